@@ -1,0 +1,325 @@
+"""Decode-attention benchmark on one MI355X: the gpt-oss KV-cache hot path.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2|3|5]
+
+A step is one pass of the hot path over the batch: KV append (RoPE on K, bf16
+store into the paged cache) plus split-K GQA flash-decoding attention (split
+and combine kernels) of one layer, for every sequence of the batch. Default
+workload: BASELINE config 2, the gpt-oss-20b-shape full-attention decode layer
+(B=512, H_q=64, H_kv=8, d=64, bf16 paged cache of 16-token blocks with a
+randomly permuted block table, context lengths U[128, 2048], values
+N(0,1)*0.5, sinks N(0,1)). Config 3 is the 128-token sliding-window layer
+(ring of 128 slots, lengths U[1, 4096]); config 5 the 36-layer gpt-oss-120b
+step (B=1024, alternating window/full layers, lengths U[1024, 3072]).
+
+Inputs are synthetic and resident in HBM before the timed region. The JSON
+line's value is algorithmic KV-read bytes per step / step time (GB/s); the
+roofline object prices the dominant kernel (the split kernel) against the 8
+TB/s HBM peak, timed with HIP events on the stream it runs on. cpu_baseline
+times the CPU oracle (a C/OpenMP restatement of run.cpp's attention) on a
+bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "optimize_inference_gpt-oss_amd")
+HBM_PEAK_GBS = 8000.0
+D = 64
+
+
+def load_gkv():
+    spec = importlib.util.spec_from_file_location("gkv", os.path.join(PKG, "gkv.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["gkv"] = mod
+    spec.loader.exec_module(mod)
+    mod.lib()
+    return mod
+
+
+CONFIGS = {
+    2: dict(name="gpt-oss-20b full-attention decode layer", B=512, Hq=64, Hkv=8, lo=128,
+            hi=2048, layers=1, window=0),
+    3: dict(name="gpt-oss sliding-window decode layer", B=512, Hq=64, Hkv=8, lo=0, hi=4095,
+            layers=1, window=128),
+    5: dict(name="gpt-oss-120b 36-layer decode step", B=1024, Hq=64, Hkv=8, lo=1024, hi=3072,
+            layers=36, window=128),
+}
+
+
+class Layer:
+    """One layer's device state: the paged cache (pool view), its inputs."""
+
+    def __init__(self, torch, gkv, pool, layer, cfg, L, seed, dev):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        B, Hq, Hkv = cfg["B"], cfg["Hq"], cfg["Hkv"]
+        self.view = pool.view(layer)
+        self.window = self.view.ring
+        self.qkv = (torch.randn(B, (Hq + 2 * Hkv) * D, generator=g, device=dev) * 0.5)
+        self.sinks = torch.randn(Hq, generator=g, device=dev)
+        self.out = torch.empty(B, Hq * D, dtype=torch.bfloat16, device=dev)
+
+
+def fill_cache(torch, gkv, pool, n_layers, dev, seed):
+    """Random bf16 N(0,1)*0.5 in every cache array of the pool (the history)."""
+    for layer in range(n_layers):
+        v = pool.view(layer)
+        for i, base in enumerate((v.k, v.v)):
+            n = v.num_blocks * v.n_kv_heads * 16 * D
+            g = torch.Generator(device=dev)
+            g.manual_seed(seed * 1000 + 2 * layer + i)
+            t = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.5, generator=g)
+            gkv.hip_memcpy_d2d(base, t.data_ptr(), n * 2)
+            torch.cuda.synchronize()
+            del t
+
+
+def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, threads):
+    """Time the CPU oracle on a bounded sample of the workload (sequences
+    0..sample_seqs-1 of layer 0) and check the GPU output on it."""
+    sys.path.insert(0, ROOT)
+    from oracle import kv_oracle as O
+
+    Hq, Hkv = cfg["Hq"], cfg["Hkv"]
+    v = layer_state.view
+    n_blk_total = v.num_blocks
+    # gather the sampled sequences' logical caches to the host
+    k_arr = gkv_cache_tensor(torch, v.k, n_blk_total, Hkv, (16, D))
+    v_arr = gkv_cache_tensor(torch, v.v, n_blk_total, Hkv, (D, 16))
+    table = table_tensor(torch, v, sample_seqs)
+    seq_lens = (L[:sample_seqs] + 1).astype(np.int32)
+    W = layer_state.window
+    S = W if W else int(seq_lens.max())
+    kc = np.zeros((sample_seqs, S, Hkv, D), np.float32)
+    vc = np.zeros((sample_seqs, S, Hkv, D), np.float32)
+    for b in range(sample_seqs):
+        n_slots = min(int(seq_lens[b]), W) if W else int(seq_lens[b])
+        nb = (n_slots + 15) // 16
+        blocks = torch.from_numpy(table[b, :nb].astype(np.int64)).to(k_arr.device)
+        kb = k_arr[blocks].float().permute(0, 2, 1, 3).reshape(nb * 16, Hkv, D)
+        vb = v_arr[blocks].float().permute(0, 3, 1, 2).reshape(nb * 16, Hkv, D)
+        kc[b, :n_slots] = kb[:n_slots].cpu().numpy()
+        vc[b, :n_slots] = vb[:n_slots].cpu().numpy()
+    qkv = layer_state.qkv[:sample_seqs].cpu().numpy()
+    cos, sin = O.rope_table(int(seq_lens.max()))
+    pos = seq_lens - 1
+    q_rot, _, _, _ = O.kv_append(qkv, Hq, Hkv, cos, sin, pos)
+    sinks = layer_state.sinks.cpu().numpy()
+    t0 = time.perf_counter()
+    ref = O.decode_attention(q_rot, kc, vc, pos, sinks, window=W, ring=W, n_threads=threads)
+    dt = time.perf_counter() - t0
+    n_read = np.minimum(seq_lens, W) if W else seq_lens
+    nbytes = float(n_read.sum()) * Hkv * D * 2 * 2
+    got = gpu_out[:sample_seqs].float().cpu().numpy().reshape(sample_seqs, Hq, D)
+    err = np.abs(got - ref)
+    ok = bool(np.all(err <= 2e-3 + 1e-2 * np.abs(ref)))
+    return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                sample=f"{sample_seqs} sequences of layer 0 ({int(n_read.sum())} cached tokens, "
+                       f"{nbytes / 1e6:.1f} MB of K+V), one decode attention, "
+                       f"{dt:.2f} s wall on {threads} OpenMP threads",
+                seconds=round(dt, 3), gpu_matches=ok, max_abs_err=float(err.max()))
+
+
+def gkv_cache_tensor(torch, ptr, num_blocks, Hkv, inner):
+    """A device copy of a pool array (bf16 [num_blocks][Hkv][inner...])."""
+    import gkv
+    n = num_blocks * Hkv * inner[0] * inner[1]
+    t = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    gkv.hip_memcpy_d2d(t.data_ptr(), ptr, n * 2)
+    return t.view(num_blocks, Hkv, *inner)
+
+
+def table_tensor(torch, view, n_rows):
+    import gkv
+    t = torch.empty(n_rows * view.table_stride, dtype=torch.int32, device="cuda")
+    gkv.hip_memcpy_d2d(t.data_ptr(), view.block_table, t.numel() * 4)
+    torch.cuda.synchronize()
+    return t.view(n_rows, view.table_stride).cpu().numpy()
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--split-tokens", type=int, default=0)
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--cpu-sample", type=int, default=128,
+                    help="sequences timed on the CPU oracle (0: skip)")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "decode attention shards over sequences or kv heads with no exchange, which "
+              "is not built here", file=sys.stderr)
+        return 2
+
+    import torch
+    gkv = load_gkv()
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[args.config]
+    B, Hq, Hkv, n_layers = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["layers"]
+    rng = np.random.default_rng(args.seed)
+    L = rng.integers(cfg["lo"], cfg["hi"] + 1, size=B).astype(np.int32)  # context lengths
+    seq_lens = L + 1
+    max_len = int(seq_lens.max())
+
+    # Paged pool sized for this batch, block ids handed out in a seeded random order.
+    need = int(((seq_lens + 15) // 16).sum())
+    pool = gkv.Pool(n_layers=n_layers, n_kv_heads=Hkv, max_seqs=B, max_seq_len=max_len,
+                    window=cfg["window"], num_blocks=need + 64, shuffle_seed=args.seed)
+    seqs = [pool.seq_alloc() for _ in range(B)]
+    assert seqs == list(range(B))  # row b of the batch is sequence id b
+    for b in range(B):
+        st = pool.reserve(b, int(seq_lens[b]))
+        if st != 0:
+            raise RuntimeError(f"pool reserve failed: {gkv.status_string(st)}")
+    pool.sync()
+    fill_cache(torch, gkv, pool, n_layers, dev, args.seed)
+
+    layers = [Layer(torch, gkv, pool, l, cfg, L, args.seed * 100 + l, dev)
+              for l in range(n_layers)]
+    cos, sin = gkv.rope_table(max(max_len, 1))
+    cos_d, sin_d = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+    pos_d = torch.from_numpy(L).to(dev)
+    lens_d = torch.from_numpy(seq_lens).to(dev)
+    err_d = torch.zeros(1, dtype=torch.int32, device=dev)
+    ws_bytes = max(gkv.workspace_bytes(B, Hkv, max_len, 0, args.split_tokens), 4)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def bytes_of(layer: Layer) -> float:
+        n = np.minimum(seq_lens, layer.window) if layer.window else seq_lens
+        return float(n.sum()) * Hkv * D * 2 * 2
+
+    kv_bytes = sum(bytes_of(l) for l in layers)
+
+    ev = {}
+
+    def step(record: bool):
+        for li, layer in enumerate(layers):
+            if record:
+                e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+                e[0].record(stream)
+            gkv.kv_append(layer.qkv, Hq, cos_d, sin_d, pos_d, layer.view, seq_lens=lens_d,
+                          dev_err=err_d, stream=stream)
+            if record:
+                e[1].record(stream)
+            gkv.decode_attention(layer.qkv, lens_d, max_len, layer.view, layer.sinks, layer.out,
+                                 window=layer.window, cos_tab=cos_d, sin_tab=sin_d,
+                                 split_tokens=args.split_tokens, workspace=ws, dev_err=err_d,
+                                 stream=stream, stage="split")
+            if record:
+                e[2].record(stream)
+            gkv.decode_attention(layer.qkv, lens_d, max_len, layer.view, layer.sinks, layer.out,
+                                 window=layer.window, split_tokens=args.split_tokens,
+                                 workspace=ws, stream=stream, stage="combine")
+            if record:
+                e[3].record(stream)
+                ev.setdefault(li, []).append(e)
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    if int(err_d.item()) != 0:
+        raise RuntimeError(f"device error word {int(err_d.item())}")
+
+    # Timed region: K steps, whole-step wall time (events only in a second pass,
+    # so that the step time carries no event overhead).
+    torch.cuda.synchronize()
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    t_start.record(stream)
+    for _ in range(args.steps):
+        step(False)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = t_start.elapsed_time(t_end) / args.steps
+
+    # Per-kernel durations (HIP events on the launch stream) over K more steps.
+    ev.clear()
+    for _ in range(args.steps):
+        step(True)
+    torch.cuda.synchronize()
+    split_ms = append_ms = combine_ms = 0.0
+    split_bytes = 0.0
+    for li, lst in ev.items():
+        a = np.mean([e[0].elapsed_time(e[1]) for e in lst])
+        s = np.mean([e[1].elapsed_time(e[2]) for e in lst])
+        c = np.mean([e[2].elapsed_time(e[3]) for e in lst])
+        append_ms += a
+        split_ms += s
+        combine_ms += c
+    # dominant kernel: the split kernel of the full-attention layers (or of the
+    # window layers when there are no full ones)
+    full = [i for i, l in enumerate(layers) if not l.window] or list(range(len(layers)))
+    dom_ms = float(np.mean([np.mean([e[1].elapsed_time(e[2]) for e in ev[i]]) for i in full]))
+    dom_bytes = float(np.mean([bytes_of(layers[i]) for i in full]))
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", f"decode_split_config{args.config}_traffic.json")
+    if os.path.exists(tpath) and not args.split_tokens:
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    cpu = None
+    if args.cpu_sample > 0:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        cpu = cpu_baseline(torch, gkv, pool, layers[full[0]], L, cfg, layers[full[0]].out,
+                           min(args.cpu_sample, B), threads)
+
+    value = kv_bytes / (ms_per_step * 1e-3) / 1e9
+    line = {
+        "metric": "decode-attn step latency + KV-read GB/s (% of HBM peak), gpt-oss-20b shape B=512",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*0.5 K/V/q, N(0,1) sinks, random-permuted block table)",
+        "config": {
+            "workload": f"config {args.config}: {cfg['name']}",
+            "B": B, "H_q": Hq, "H_kv": Hkv, "head_dim": D, "layers": n_layers,
+            "context": f"U[{cfg['lo']},{cfg['hi']}]", "window": cfg["window"],
+            "kv_bytes_per_step": kv_bytes, "split_tokens": args.split_tokens or 512,
+            "pool_bytes": pool.device_bytes(),
+            "kernel_ms": {"append": round(append_ms, 4), "split": round(split_ms, 4),
+                          "combine": round(combine_ms, 4)},
+            "parallelism": "1 GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "decode_split_kernel",
+            "kernel_us": round(dom_ms * 1e3, 2),
+            "algorithmic_bytes": dom_bytes,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    pool.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,217 @@
+/* gkv: the gpt-oss KV-cache hot path on MI355X (gfx950), C ABI.
+ *
+ * Paged bf16 KV cache, KV append with RoPE on K, split-K GQA flash-decoding
+ * with per-head sink logits and a sliding window, the cross-split combine, and
+ * a causal prefill-chunk attention. Plain pointers and sizes only; every call
+ * returns a gkv_status; nothing here exits or throws. Kernel entry points
+ * enqueue on the given HIP stream (hipStream_t passed as void*; NULL = the
+ * null stream) and never allocate device memory.
+ *
+ * Reference interfaces replaced (n30nd/Optimize_Inference_GPT-OSS):
+ *   gkv_rope_table        <- compute_cos_sin host table, getp-csrc/engine/gpu_engine.hpp:388-396
+ *                            (run.cpp:422-504)
+ *   gkv_kv_append         <- rope_kv_bf16, getp-csrc/kernels/fast_misc.hpp:112-127
+ *                            (and rope_exact + kv_write_kernel, kernels/misc.hpp:55-85)
+ *   gkv_decode_attention  <- attention_q8v_chunk64 / attention_bf16_chunk64 / attention_bf16,
+ *                            getp-csrc/kernels/fast_attention.hpp:604-622, 566-580, 525-547
+ *   gkv_decode_split, gkv_decode_combine
+ *                         <- the per-wave split and the LDS merge inside
+ *                            attention_gqa8_kernel, fast_attention.hpp:164-425 (a7: 383-424)
+ *   gkv_prefill_attention <- no reference kernel; the reference feeds prompts one
+ *                            token at a time through the decode step
+ *                            (gpu_engine.hpp:811-813); same semantics per position
+ *   gkv_pool_*            <- KV allocation in gpu_alloc_state, gpu_engine.hpp:306-334,
+ *                            and its sizing/regrow (gpu_fit_batch :425-433, :921-927)
+ *
+ * Layouts (device memory):
+ *   qkv rows     fp32 [Q (Hq*64) | K (Hkv*64) | V (Hkv*64)], row stride in floats
+ *                (fast_misc.hpp:57-58)
+ *   K cache      bf16 [num_blocks][Hkv][block_tokens=16][64]
+ *   V cache      bf16 [num_blocks][Hkv][64][16]  (transposed inside a block)
+ *   block table  int32 [B][table_stride]: logical block j of sequence b -> physical block
+ *   ring layers  (sliding window W, W % 16 == 0): position p lives in slot p % W, the
+ *                table row holds W/16 blocks (gpu_engine.hpp:477, misc.hpp:72-85)
+ */
+#ifndef GKV_H
+#define GKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  GKV_OK = 0,
+  GKV_ERR_ARG = -1,         /* bad argument (null pointer, negative size, ...) */
+  GKV_ERR_UNSUPPORTED = -2, /* shape the kernels do not implement (head_dim != 64, ...) */
+  GKV_ERR_CAPACITY = -3,    /* pool out of blocks, or a length beyond a table's capacity */
+  GKV_ERR_BLOCK = -4,       /* invalid block id / sequence id */
+  GKV_ERR_HIP = -5,         /* a HIP runtime call failed */
+  GKV_ERR_WORKSPACE = -6    /* workspace smaller than gkv_decode_workspace_bytes() */
+} gkv_status;
+
+/* Bits of the device error word that kernels OR in when they meet bad data
+ * (they never fault on it: the token is treated as absent). */
+#define GKV_DEVERR_BLOCK_ID 1u /* a table entry outside [0, num_blocks) */
+#define GKV_DEVERR_LENGTH 2u   /* a sequence length beyond the table's capacity */
+
+typedef enum { GKV_F32 = 0, GKV_BF16 = 1 } gkv_dtype;
+
+/* A paged cache of one layer as the kernels see it. */
+typedef struct {
+  void *k;                     /* bf16 [num_blocks][n_kv_heads][16][64] */
+  void *v;                     /* bf16 [num_blocks][n_kv_heads][64][16] */
+  const int32_t *block_table;  /* int32 [B][table_stride] (device) */
+  int32_t table_stride;        /* entries per table row */
+  int32_t num_blocks;          /* physical blocks in k / v (ids are checked against it) */
+  int32_t n_kv_heads;
+  int32_t ring;                /* 0: slot = position; W > 0: slot = position % W */
+} gkv_cache_view;
+
+const char *gkv_status_string(int status);
+/* Library version, "major.minor.patch". */
+const char *gkv_version(void);
+
+/* ---- RoPE angles (host) ------------------------------------------------- */
+
+typedef struct {
+  float base;                   /* rope_theta (150000) */
+  int32_t head_dim;             /* 64 */
+  float scaling_factor;         /* 32 */
+  float initial_context_length; /* 4096 */
+  float ntk_beta;               /* 32 */
+  float ntk_alpha;              /* 1 */
+} gkv_rope_config;
+
+/* Host table [n_pos][head_dim/2] of cos and sin, bit-identical to the
+ * reference's compute_cos_sin(pos, ...) for pos = 0..n_pos-1. */
+int gkv_rope_table(const gkv_rope_config *cfg, int32_t n_pos, float *cos_tab, float *sin_tab);
+
+/* ---- KV append ----------------------------------------------------------- */
+
+/* RoPE on K of each row, then bf16 (round to nearest even) K and V stored into
+ * the paged cache at the row's slot. One row per token:
+ *   row_pos[r]   position of row r's token (device int32)
+ *   row_seq[r]   its sequence (device int32; NULL: row r is sequence r)
+ *   seq_lens[s]  tokens of sequence s after this append (device int32; NULL:
+ *                none). Only used on ring layers: a row whose slot a later
+ *                row of this same call overwrites (pos + ring < seq_len) is
+ *                not stored, so the ring ends up holding the last W positions.
+ *   q_out        NULL, or fp32 [rows][q_out_stride] receiving the rotated Q
+ *                (may equal qkv with q_out_stride = row_stride: in place)
+ *   k_pack/v_pack NULL, or bf16 [rows][Hkv][64] receiving the same bf16 K, V
+ *                (the packed operands of gkv_prefill_attention)
+ *   dev_err      NULL, or a device uint32 that gets GKV_DEVERR_* bits
+ * cos_tab/sin_tab: device copies of gkv_rope_table rows. */
+int gkv_kv_append(void *stream, int32_t n_rows, const float *qkv, int64_t row_stride,
+                  int32_t n_q_heads, const float *cos_tab, const float *sin_tab,
+                  const int32_t *row_pos, const int32_t *row_seq, const int32_t *seq_lens,
+                  gkv_cache_view cache, float *q_out, int64_t q_out_stride, void *k_pack,
+                  void *v_pack, uint32_t *dev_err);
+
+/* ---- Decode attention ---------------------------------------------------- */
+
+/* Bytes of workspace gkv_decode_attention / gkv_decode_split need. */
+size_t gkv_decode_workspace_bytes(int32_t B, int32_t n_kv_heads, int32_t max_seq_len,
+                                  int32_t window, int32_t split_tokens);
+
+/* One query token per sequence against its cached keys/values plus the head's
+ * sink logit (run.cpp:597-642 semantics):
+ *   q         fp32 [B][q_stride], heads at h*64; not yet rotated if cos_tab is
+ *             given (rotated on load with row seq_lens[b]-1, bit-identical to
+ *             the append's rotation), already rotated if cos_tab is NULL
+ *   seq_lens  device int32 [B]: tokens in the cache (the new one included)
+ *   window    0: full attention over all seq_len tokens; W > 0: the last
+ *             min(seq_len, W) tokens (cache.ring must be W or 0)
+ *   sinks     fp32 [Hq]
+ *   split_tokens  tokens per workgroup split (multiple of 128; 0 = default)
+ *   max_seq_len   host upper bound of seq_lens (sizes the grid)
+ *   out       [B][out_stride] of out_dtype, heads at h*64
+ * Launches gkv_decode_split then, when some sequence has more than one split,
+ * gkv_decode_combine. */
+int gkv_decode_attention(void *stream, int32_t B, int32_t n_q_heads, const float *q,
+                         int64_t q_stride, const float *cos_tab, const float *sin_tab,
+                         const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,
+                         int32_t window, const float *sinks, int32_t split_tokens,
+                         void *workspace, size_t workspace_bytes, void *out, int64_t out_stride,
+                         int32_t out_dtype, uint32_t *dev_err);
+
+/* The two stages of gkv_decode_attention, for callers that time or schedule
+ * them separately. Same arguments. gkv_decode_split writes the final output of
+ * every sequence that fits in one split, and per-split partial results of the
+ * others into the workspace; gkv_decode_combine merges those with the sink. */
+int gkv_decode_split(void *stream, int32_t B, int32_t n_q_heads, const float *q,
+                     int64_t q_stride, const float *cos_tab, const float *sin_tab,
+                     const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,
+                     int32_t window, const float *sinks, int32_t split_tokens, void *workspace,
+                     size_t workspace_bytes, void *out, int64_t out_stride, int32_t out_dtype,
+                     uint32_t *dev_err);
+int gkv_decode_combine(void *stream, int32_t B, int32_t n_q_heads, int32_t n_kv_heads,
+                       const int32_t *seq_lens, int32_t max_seq_len, int32_t window,
+                       const float *sinks, int32_t split_tokens, const void *workspace,
+                       size_t workspace_bytes, void *out, int64_t out_stride, int32_t out_dtype);
+
+/* ---- Prefill (causal) attention ----------------------------------------- */
+
+/* Causal attention of packed prompts with sinks: row j of prompt b (rows
+ * cu_seqlens[b] .. cu_seqlens[b+1]-1, positions 0..L_b-1) attends to rows
+ * 0..j of its prompt (window W: j-W+1..j):
+ *   q        fp32 [rows][q_stride], rotated (gkv_kv_append's q_out)
+ *   k, v     bf16 [rows][Hkv][64] (gkv_kv_append's k_pack, v_pack)
+ *   cu_seqlens device int32 [B+1]; max_len = host bound of the prompt lengths
+ *   out      [rows][out_stride] of out_dtype */
+int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_seqlens, int32_t max_len,
+                          int32_t n_q_heads, int32_t n_kv_heads, const float *q,
+                          int64_t q_stride, const void *k, const void *v, const float *sinks,
+                          int32_t window, void *out, int64_t out_stride, int32_t out_dtype);
+
+/* ---- Paged KV pool (host bookkeeping, device storage) -------------------- */
+
+typedef struct gkv_pool gkv_pool;
+
+typedef struct {
+  int32_t n_layers;        /* layers; layer l is a window layer iff window > 0 and l % 2 == 0
+                              (run.cpp:617-619, gpu_engine.hpp:318) */
+  int32_t n_kv_heads;
+  int32_t head_dim;        /* 64 */
+  int32_t window;          /* sliding window W (multiple of 16), 0 = none */
+  int32_t max_seqs;        /* sequence ids 0 .. max_seqs-1 */
+  int32_t max_seq_len;     /* longest sequence (sizes the table rows) */
+  int64_t num_blocks;      /* physical 16-token blocks for the full layers; 0: derive from
+                              bytes_budget */
+  int64_t bytes_budget;    /* used when num_blocks == 0: device bytes for all caches;
+                              0: 90% of hipMemGetInfo's free memory */
+  uint64_t shuffle_seed;   /* 0: blocks handed out in id order; else a seeded
+                              permutation (scattered physical placement) */
+} gkv_pool_config;
+
+int gkv_pool_create(const gkv_pool_config *cfg, gkv_pool **out);
+int gkv_pool_destroy(gkv_pool *pool);
+/* Takes a free sequence id (its length starts at 0). */
+int gkv_pool_seq_alloc(gkv_pool *pool, int32_t *seq_id);
+/* Makes room for seq_len tokens of seq_id (allocating blocks; never shrinks). */
+int gkv_pool_seq_reserve(gkv_pool *pool, int32_t seq_id, int32_t seq_len);
+/* Returns the sequence's blocks to the free list. */
+int gkv_pool_seq_free(gkv_pool *pool, int32_t seq_id);
+/* Copies the host block tables to the device (after alloc/reserve/free). */
+int gkv_pool_sync(gkv_pool *pool, void *stream);
+/* Cache view of layer l over the table rows of sequence ids 0 .. max_seqs-1
+ * (rows of the batch must be sequence ids: pass row_seq or order the batch by id). */
+int gkv_pool_layer_view(const gkv_pool *pool, int32_t layer, gkv_cache_view *view);
+/* Table-row view starting at sequence id first_seq (for batches of consecutive ids). */
+int gkv_pool_layer_view_from(const gkv_pool *pool, int32_t layer, int32_t first_seq,
+                             gkv_cache_view *view);
+int64_t gkv_pool_free_blocks(const gkv_pool *pool);
+int64_t gkv_pool_num_blocks(const gkv_pool *pool);
+/* Device bytes held by the pool's caches and tables. */
+int64_t gkv_pool_device_bytes(const gkv_pool *pool);
+/* Host copy of a sequence's full-layer table row (n entries at most). */
+int gkv_pool_seq_blocks(const gkv_pool *pool, int32_t seq_id, int32_t *blocks, int32_t n,
+                        int32_t *n_used);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GKV_H */

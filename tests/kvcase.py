@@ -1,0 +1,126 @@
+"""Seeded decode cases: a paged cache with history, the new token's qkv row,
+and what the CPU oracle says the append and the attention must produce.
+
+The physical placement is a random permutation of block ids; every slot and
+block that holds no token is poisoned with bf16 NaN (0x7fc0), so a kernel that
+reads or writes outside its tokens shows up as a NaN or a changed byte.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import kv_oracle as O
+
+D = 64
+BT = 16
+BF16_NAN = 0x7FC0
+
+
+class DecodeCase:
+    def __init__(self, B, n_q_heads, n_kv_heads, ctx_lens, window=0, scale=1.0, seed=0,
+                 extra_blocks=7, rope_rows=None, sink_scale=1.0):
+        rng = np.random.default_rng(seed)
+        self.B, self.Hq, self.Hkv = B, n_q_heads, n_kv_heads
+        self.window = window
+        self.ring = window
+        self.L = np.asarray(ctx_lens, np.int32)      # context before the append
+        assert self.L.shape == (B,)
+        self.pos = self.L.copy()                     # position of the new token
+        self.seq_lens = self.L + 1
+        kvd = n_kv_heads * D
+        self.row_width = (n_q_heads + 2 * n_kv_heads) * D
+        self.qkv = (rng.standard_normal((B, self.row_width)) * scale).astype(np.float32)
+        self.sinks = (rng.standard_normal(n_q_heads) * sink_scale).astype(np.float32)
+        n_rope = rope_rows if rope_rows is not None else int(self.pos.max()) + 1
+        self.cos, self.sin = O.rope_table(n_rope)
+
+        # Block tables.
+        if self.ring:
+            per_seq = np.full(B, self.ring // BT, np.int32)
+        else:
+            per_seq = (self.seq_lens + BT - 1) // BT
+        self.table_stride = int(per_seq.max())
+        self.num_blocks = int(per_seq.sum()) + extra_blocks
+        ids = rng.permutation(self.num_blocks).astype(np.int32)
+        self.table = np.full((B, self.table_stride), -1, np.int32)
+        o = 0
+        for b in range(B):
+            self.table[b, :per_seq[b]] = ids[o:o + per_seq[b]]
+            o += per_seq[b]
+
+        # Caches, poisoned.
+        self.k = np.full((self.num_blocks, n_kv_heads, BT, D), BF16_NAN, np.uint16)
+        self.v = np.full((self.num_blocks, n_kv_heads, D, BT), BF16_NAN, np.uint16)
+        # Oracle's logical cache (slot-indexed fp32 of the bf16 values).
+        S = self.ring if self.ring else int(self.seq_lens.max())
+        self.S = S
+        self.kc = np.zeros((B, S, n_kv_heads, D), np.float32)
+        self.vc = np.zeros((B, S, n_kv_heads, D), np.float32)
+        for b in range(B):
+            L = int(self.L[b])
+            if self.ring:
+                # Tokens the ring holds before this append: L-W .. L-1 (the
+                # oldest is overwritten by the new token).
+                t_hist = np.arange(max(0, L - self.ring), L)
+            else:
+                t_hist = np.arange(0, L)
+            if len(t_hist) == 0:
+                continue
+            kh = O.to_bf16(rng.standard_normal((len(t_hist), n_kv_heads, D)) * scale)
+            vh = O.to_bf16(rng.standard_normal((len(t_hist), n_kv_heads, D)) * scale)
+            slots = t_hist % self.ring if self.ring else t_hist
+            self._place(b, slots, kh, vh)
+            self.kc[b, slots] = O.from_bf16(kh)
+            self.vc[b, slots] = O.from_bf16(vh)
+
+        # The append, per the oracle.
+        q_rot, _, kb, vb = O.kv_append(self.qkv, n_q_heads, n_kv_heads, self.cos, self.sin,
+                                       self.pos)
+        self.q_rot = q_rot
+        self.k_expect = self.k.copy()
+        self.v_expect = self.v.copy()
+        for b in range(B):
+            slot = int(self.pos[b] % self.ring) if self.ring else int(self.pos[b])
+            phys = self.table[b, slot // BT]
+            self.k_expect[phys, :, slot % BT, :] = kb[b]
+            self.v_expect[phys, :, :, slot % BT] = vb[b]
+            self.kc[b, slot] = O.from_bf16(kb[b])
+            self.vc[b, slot] = O.from_bf16(vb[b])
+        del kvd
+
+    def _place(self, b, slots, kh, vh):
+        phys = self.table[b, slots // BT]
+        off = slots % BT
+        self.k[phys, :, off, :] = kh
+        # v[phys, g, :, off] = vh[j, g, :]
+        self.v[phys, :, :, off] = vh
+
+    def oracle_out(self, n_threads=0):
+        return O.decode_attention(self.q_rot, self.kc, self.vc, self.pos, self.sinks,
+                                  window=self.window, ring=self.ring, n_threads=n_threads)
+
+    # ---- device side ------------------------------------------------------
+    def to_device(self, torch, device, cos=None, sin=None):
+        """Tensors for the GPU path. cos/sin: the product's host table (defaults
+        to the oracle's, which is bit-identical)."""
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+        dev = {
+            "qkv": t(self.qkv),
+            "sinks": t(self.sinks),
+            "cos": t(self.cos if cos is None else cos),
+            "sin": t(self.sin if sin is None else sin),
+            "pos": t(self.pos),
+            "seq_lens": t(self.seq_lens),
+            "table": t(self.table),
+            "k": t(self.k.view(np.int16)),
+            "v": t(self.v.view(np.int16)),
+            "err": torch.zeros(1, dtype=torch.int32, device=device),
+        }
+        return dev
+
+
+def allclose_report(got, ref, atol=2e-3, rtol=1e-2):
+    err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    bound = atol + rtol * np.abs(ref.astype(np.float64))
+    bad = ~(err <= bound)
+    return int(bad.sum()), float(np.nanmax(err)) if err.size else 0.0

@@ -1,0 +1,117 @@
+"""libgkv.so on the CPU: it loads, exports every entry point of include/gkv.h,
+its host RoPE table is the reference's, and it rejects bad arguments before
+touching the GPU."""
+import ctypes
+import os
+import re
+
+import numpy as np
+
+from oracle import kv_oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "gkv.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gkv_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_function(gkv):
+    names = header_functions()
+    assert len(names) >= 20
+    lib = gkv.lib()
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(gkv.SIGNATURES), set(names) ^ set(gkv.SIGNATURES)
+
+
+def test_status_strings(gkv):
+    assert gkv.status_string(0) == "ok"
+    for st in range(-6, 0):
+        assert gkv.status_string(st) not in ("ok", "unknown status")
+    assert gkv.lib().gkv_version().decode().count(".") == 2
+
+
+def test_rope_table_bit_exact_vs_oracle_and_golden(gkv, golden):
+    c, s = gkv.rope_table(4097)
+    oc, os_ = O.rope_table(4097)
+    assert np.array_equal(c.view(np.uint32), oc.view(np.uint32))
+    assert np.array_equal(s.view(np.uint32), os_.view(np.uint32))
+    pos = golden["table_positions"]
+    assert np.array_equal(c[pos].view(np.uint32), golden["table_cos"].view(np.uint32))
+    assert np.array_equal(s[pos].view(np.uint32), golden["table_sin"].view(np.uint32))
+
+
+def test_rope_table_without_scaling(gkv):
+    c, s = gkv.rope_table(10, scaling_factor=1.0)
+    inv = 1.0 / np.float32(150000.0) ** (np.arange(32, dtype=np.float32) * 2 / 64)
+    assert np.allclose(c[9], np.cos(9 * inv), atol=1e-5)
+
+
+def test_rope_table_rejects_bad_args(gkv):
+    cfg = gkv.RopeConfig(**gkv.GPT_OSS_ROPE)
+    buf = np.zeros(64, np.float32)
+    assert gkv.lib().gkv_rope_table(ctypes.byref(cfg), -1, buf.ctypes.data, buf.ctypes.data) == gkv.GKV_ERR_ARG
+    assert gkv.lib().gkv_rope_table(None, 1, buf.ctypes.data, buf.ctypes.data) == gkv.GKV_ERR_ARG
+    cfg.head_dim = 63
+    assert gkv.lib().gkv_rope_table(ctypes.byref(cfg), 1, buf.ctypes.data, buf.ctypes.data) == gkv.GKV_ERR_ARG
+
+
+def _view(gkv, **kw):
+    d = dict(k=1, v=1, block_table=1, table_stride=4, num_blocks=8, n_kv_heads=8, ring=0)
+    d.update(kw)
+    return gkv.CacheView(**d)
+
+
+def test_append_argument_checks(gkv):
+    L = gkv.lib()
+    fake = 0x1000  # never dereferenced: the checks fail first
+    args = lambda **o: dict(dict(stream=None, n=4, qkv=fake, stride=80 * 64, hq=64, cos=fake,
+                                 sin=fake, pos=fake, seq=None, lens=None, view=_view(gkv),
+                                 q_out=None, q_stride=0, kp=None, vp=None, err=None), **o)
+    def call(a):
+        return L.gkv_kv_append(a["stream"], a["n"], a["qkv"], a["stride"], a["hq"], a["cos"],
+                               a["sin"], a["pos"], a["seq"], a["lens"], a["view"], a["q_out"],
+                               a["q_stride"], a["kp"], a["vp"], a["err"])
+    assert call(args(n=-1)) == gkv.GKV_ERR_ARG
+    assert call(args(qkv=None)) == gkv.GKV_ERR_ARG
+    assert call(args(stride=64)) == gkv.GKV_ERR_ARG            # row shorter than q|k|v
+    assert call(args(hq=60)) == gkv.GKV_ERR_ARG                # not a multiple of Hkv
+    assert call(args(view=_view(gkv, ring=100))) == gkv.GKV_ERR_UNSUPPORTED
+    assert call(args(view=_view(gkv, num_blocks=0))) == gkv.GKV_ERR_ARG
+    assert call(args(n=0)) == gkv.GKV_OK                        # nothing to do
+
+
+def test_decode_argument_checks(gkv):
+    L = gkv.lib()
+    fake = 0x1000
+    def call(B=4, hq=64, max_len=100, view=None, window=0, split=0, ws=None, ws_bytes=0,
+             out_stride=4096, dtype=0, q=fake, lens=fake):
+        return L.gkv_decode_attention(None, B, hq, q, 4096 + 1024, None, None, lens, max_len,
+                                      view or _view(gkv), window, fake, split, ws, ws_bytes,
+                                      fake, out_stride, dtype, None)
+    assert call(B=-1) == gkv.GKV_ERR_ARG
+    assert call(q=None) == gkv.GKV_ERR_ARG
+    assert call(lens=None) == gkv.GKV_ERR_ARG
+    assert call(hq=128 + 8) == gkv.GKV_ERR_UNSUPPORTED          # 17 query heads per kv head
+    assert call(split=100) == gkv.GKV_ERR_ARG                   # not a multiple of 128
+    assert call(out_stride=100) == gkv.GKV_ERR_ARG
+    assert call(dtype=7) == gkv.GKV_ERR_ARG
+    assert call(view=_view(gkv, ring=128), window=0) == gkv.GKV_ERR_ARG
+    assert call(view=_view(gkv, ring=64), window=128) == gkv.GKV_ERR_ARG
+    # long sequences need a workspace of the advertised size
+    need = gkv.workspace_bytes(4, 8, 5000)
+    assert need > 0
+    assert call(max_len=5000) == gkv.GKV_ERR_WORKSPACE
+    assert call(max_len=5000, ws=fake, ws_bytes=need - 1) == gkv.GKV_ERR_WORKSPACE
+    assert call(B=0, max_len=5000, ws=fake, ws_bytes=need) == gkv.GKV_OK
+    # a window layer never splits past its window
+    assert gkv.workspace_bytes(512, 8, 4096, window=128) == 0
+
+
+def test_workspace_formula(gkv):
+    # splits of 512 tokens: (B * Hkv * splits) partials of 8x64 + 16 floats
+    assert gkv.workspace_bytes(2, 8, 1025, split_tokens=512) == 2 * 8 * 3 * (512 + 16) * 4
+    assert gkv.workspace_bytes(2, 8, 512, split_tokens=512) == 0
