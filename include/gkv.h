@@ -71,6 +71,8 @@ typedef struct {
 } gkv_cache_view;
 
 const char *gkv_status_string(int status);
+/* Text of the last HIP error a gkv call on this thread met ("" if none). */
+const char *gkv_last_error(void);
 /* Library version, "major.minor.patch". */
 const char *gkv_version(void);
 

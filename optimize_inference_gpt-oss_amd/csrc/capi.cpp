@@ -1,5 +1,25 @@
 // Status strings and version of the gkv C ABI.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <string>
+
 #include "gkv.h"
+
+namespace gkv {
+static thread_local std::string g_last_error;
+
+int hip_status(hipError_t e, const char *where) {
+  if (e == hipSuccess)
+    return GKV_OK;
+  char buf[256];
+  snprintf(buf, sizeof buf, "%s: %s (%d)", where, hipGetErrorString(e), (int)e);
+  g_last_error = buf;
+  return GKV_ERR_HIP;
+}
+} // namespace gkv
+
+extern "C" const char *gkv_last_error(void) { return gkv::g_last_error.c_str(); }
 
 extern "C" const char *gkv_status_string(int status) {
   switch (status) {

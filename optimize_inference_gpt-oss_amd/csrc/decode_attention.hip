@@ -228,7 +228,7 @@ __global__ __launch_bounds__(64 * NW) void decode_split_kernel(DecodeArgs a) {
     if (valid_cur < kStep || bad_cur) {
       // Tail of the sequence or a bad block id: those tokens get weight 0 and
       // their values (possibly never written) are replaced by zeros.
-      if (bad_cur && threadIdx.x == 0 && a.dev_err)
+      if (bad_cur && lane == 0 && a.dev_err)
         atomicOr(a.dev_err, GKV_DEVERR_BLOCK_ID);
       const bool blk_bad = (bad_cur >> v_blk) & 1;
 #pragma unroll
@@ -476,7 +476,7 @@ extern "C" int gkv_decode_split(void *stream, int32_t B, int32_t n_q_heads, cons
     return st;
   hipLaunchKernelGGL(decode_split_kernel<kWaves>, dim3(a.max_splits, cache.n_kv_heads, B),
                      dim3(64 * kWaves), 0, (hipStream_t)stream, a);
-  return hipGetLastError() == hipSuccess ? GKV_OK : GKV_ERR_HIP;
+  return launch_status(__func__);
 }
 
 extern "C" int gkv_decode_combine(void *stream, int32_t B, int32_t n_q_heads, int32_t n_kv_heads,
@@ -497,7 +497,7 @@ extern "C" int gkv_decode_combine(void *stream, int32_t B, int32_t n_q_heads, in
     return st;
   hipLaunchKernelGGL(decode_combine_kernel, dim3(n_kv_heads, B), dim3(256), 0,
                      (hipStream_t)stream, a);
-  return hipGetLastError() == hipSuccess ? GKV_OK : GKV_ERR_HIP;
+  return launch_status(__func__);
 }
 
 extern "C" int gkv_decode_attention(void *stream, int32_t B, int32_t n_q_heads, const float *q,
@@ -515,13 +515,13 @@ extern "C" int gkv_decode_attention(void *stream, int32_t B, int32_t n_q_heads, 
     return st;
   hipLaunchKernelGGL(decode_split_kernel<kWaves>, dim3(a.max_splits, cache.n_kv_heads, B),
                      dim3(64 * kWaves), 0, (hipStream_t)stream, a);
-  if (hipGetLastError() != hipSuccess)
-    return GKV_ERR_HIP;
+  if (int st2 = launch_status("decode_split_kernel"))
+    return st2;
   if (a.max_splits > 1) {
     hipLaunchKernelGGL(decode_combine_kernel, dim3(cache.n_kv_heads, B), dim3(256), 0,
                        (hipStream_t)stream, a);
-    if (hipGetLastError() != hipSuccess)
-      return GKV_ERR_HIP;
+    if (int st2 = launch_status("decode_combine_kernel"))
+      return st2;
   }
   return GKV_OK;
 }

@@ -47,3 +47,10 @@ __device__ __forceinline__ float swap8(float x) {
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 } // namespace gkv
+
+namespace gkv {
+// Host side: turns the launch status into a gkv_status, keeping the HIP error
+// text for gkv_last_error() (thread-local).
+int hip_status(hipError_t e, const char *where);
+inline int launch_status(const char *where) { return hip_status(hipGetLastError(), where); }
+} // namespace gkv

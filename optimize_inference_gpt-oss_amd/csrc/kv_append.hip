@@ -155,5 +155,5 @@ extern "C" int gkv_kv_append(void *stream, int32_t n_rows, const float *qkv, int
   a.v_pack = (uint16_t *)v_pack;
   a.dev_err = dev_err;
   hipLaunchKernelGGL(kv_append_kernel, dim3(n_rows), dim3(256), 0, (hipStream_t)stream, a);
-  return hipGetLastError() == hipSuccess ? GKV_OK : GKV_ERR_HIP;
+  return launch_status(__func__);
 }

@@ -55,6 +55,7 @@ GPT_OSS_ROPE = dict(base=150000.0, head_dim=64, scaling_factor=32.0,
 SIGNATURES = {
     "gkv_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "gkv_version": (ctypes.c_char_p, []),
+    "gkv_last_error": (ctypes.c_char_p, []),
     "gkv_rope_table": (ctypes.c_int, [ctypes.POINTER(RopeConfig), _i32, _vp, _vp]),
     "gkv_kv_append": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
                                      CacheView, _vp, _i64, _vp, _vp, _vp]),
@@ -88,7 +89,8 @@ _lib = None
 
 class GkvError(RuntimeError):
     def __init__(self, fn: str, status: int):
-        super().__init__(f"{fn}: {status_string(status)} ({status})")
+        detail = lib().gkv_last_error().decode() if status == GKV_ERR_HIP else ""
+        super().__init__(f"{fn}: {status_string(status)} ({status}) {detail}")
         self.status = status
 
 
@@ -96,6 +98,14 @@ def lib():
     """Load libgkv.so; raises if it has not been built."""
     global _lib
     if _lib is None:
+        # One HIP runtime per process: torch ships its own libamdhip64.so.7;
+        # loading it first makes libgkv.so bind to that same runtime (its
+        # NEEDED soname is already satisfied), so torch streams and device
+        # pointers are valid in both.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first "
                                "(there is no fallback path)")
@@ -134,7 +144,8 @@ def hip_memcpy_d2d(dst: int, src: int, nbytes: int) -> None:
     fill or read pool arrays, which are not torch tensors)."""
     global _hip
     if _hip is None:
-        _hip = ctypes.CDLL("libamdhip64.so")
+        lib()  # binds the process's HIP runtime first
+        _hip = ctypes.CDLL("libamdhip64.so.7")
         _hip.hipMemcpy.restype = ctypes.c_int
         _hip.hipMemcpy.argtypes = [_vp, _vp, _sz, ctypes.c_int]
     st = _hip.hipMemcpy(dst, src, nbytes, 3)  # hipMemcpyDeviceToDevice
