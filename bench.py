@@ -146,6 +146,27 @@ def table_tensor(torch, view, n_rows):
     return t.view(n_rows, view.table_stride).cpu().numpy()
 
 
+def copy_calibration(torch, args) -> int:
+    """A plain device copy of known size: read N bytes, write N bytes per launch."""
+    n = args.copy_mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "ms": round(ms, 4),
+                      "gbs_read_plus_write": round(2 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -157,6 +178,14 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=128,
                     help="sequences timed on the CPU oracle (0: skip)")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--lengths", default="random", choices=["random", "sorted", "fixed"],
+                    help="diagnostics: context lengths in batch order as drawn, sorted "
+                         "longest first, or all equal to the mean")
+    ap.add_argument("--sequential-blocks", action="store_true",
+                    help="diagnostics: hand out physical blocks in id order (no shuffle)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="calibration mode: time a plain device copy of this many MiB "
+                         "(the reference kernel for scaling rocprofv3 FETCH/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -165,19 +194,26 @@ def main() -> int:
         return 2
 
     import torch
+    if args.copy_mib:
+        return copy_calibration(torch, args)
     gkv = load_gkv()
     dev = torch.device("cuda:0")
     cfg = CONFIGS[args.config]
     B, Hq, Hkv, n_layers = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["layers"]
     rng = np.random.default_rng(args.seed)
     L = rng.integers(cfg["lo"], cfg["hi"] + 1, size=B).astype(np.int32)  # context lengths
+    if args.lengths == "sorted":
+        L = np.sort(L)[::-1].copy()
+    elif args.lengths == "fixed":
+        L = np.full(B, int(round(L.mean())), np.int32)
     seq_lens = L + 1
     max_len = int(seq_lens.max())
 
     # Paged pool sized for this batch, block ids handed out in a seeded random order.
     need = int(((seq_lens + 15) // 16).sum())
     pool = gkv.Pool(n_layers=n_layers, n_kv_heads=Hkv, max_seqs=B, max_seq_len=max_len,
-                    window=cfg["window"], num_blocks=need + 64, shuffle_seed=args.seed)
+                    window=cfg["window"], num_blocks=need + 64,
+                    shuffle_seed=0 if args.sequential_blocks else args.seed)
     seqs = [pool.seq_alloc() for _ in range(B)]
     assert seqs == list(range(B))  # row b of the batch is sequence id b
     for b in range(B):

@@ -128,7 +128,9 @@ size_t gkv_decode_workspace_bytes(int32_t B, int32_t n_kv_heads, int32_t max_seq
  *   window    0: full attention over all seq_len tokens; W > 0: the last
  *             min(seq_len, W) tokens (cache.ring must be W or 0)
  *   sinks     fp32 [Hq]
- *   split_tokens  tokens per workgroup split (multiple of 128; 0 = default)
+ *   split_tokens  0: balanced (the total is cut into equal ranges, one per
+ *             workgroup the GPU holds at once); > 0: ranges of this many tokens
+ *             (a multiple of 32, at most 4096)
  *   max_seq_len   host upper bound of seq_lens (sizes the grid)
  *   out       [B][out_stride] of out_dtype, heads at h*64
  * Launches gkv_decode_split then, when some sequence has more than one split,

@@ -15,6 +15,14 @@ constexpr float kLog2e = 1.4426950408889634f;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Buffer resource over the 2 KB of one head of one paged block: loads take a
+// scalar base and a 32-bit per-lane offset; reads past 2 KB return zero.
+// Word 3 = 0x00020000: 32-bit data format, the gfx9-family raw-buffer setting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const void *base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 2048, 0x00020000);
+}
 
 // fp32 -> bf16 bits, round to nearest even, NaN kept quiet. Written out in
 // integer form so the stored cache bits follow this rule exactly

@@ -10,7 +10,8 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libgkv.so")
+# GKV_LIB overrides the library path (for trying a differently built libgkv.so).
+LIB_PATH = os.environ.get("GKV_LIB") or os.path.join(HERE, "libgkv.so")
 
 GKV_OK = 0
 GKV_ERR_ARG = -1

@@ -101,17 +101,20 @@ def test_decode_argument_checks(gkv):
     assert call(dtype=7) == gkv.GKV_ERR_ARG
     assert call(view=_view(gkv, ring=128), window=0) == gkv.GKV_ERR_ARG
     assert call(view=_view(gkv, ring=64), window=128) == gkv.GKV_ERR_ARG
-    # long sequences need a workspace of the advertised size
+    # a workspace of the advertised size is required
     need = gkv.workspace_bytes(4, 8, 5000)
     assert need > 0
     assert call(max_len=5000) == gkv.GKV_ERR_WORKSPACE
     assert call(max_len=5000, ws=fake, ws_bytes=need - 1) == gkv.GKV_ERR_WORKSPACE
     assert call(B=0, max_len=5000, ws=fake, ws_bytes=need) == gkv.GKV_OK
-    # a window layer never splits past its window
-    assert gkv.workspace_bytes(512, 8, 4096, window=128) == 0
+    # more fixed-size ranges than the workspace holds
+    assert call(B=4, max_len=1 << 20, split=32, ws=fake, ws_bytes=need) == gkv.GKV_ERR_ARG
 
 
 def test_workspace_formula(gkv):
-    # splits of 512 tokens: (B * Hkv * splits) partials of 8x64 + 16 floats
-    assert gkv.workspace_bytes(2, 8, 1025, split_tokens=512) == 2 * 8 * 3 * (512 + 16) * 4
-    assert gkv.workspace_bytes(2, 8, 512, split_tokens=512) == 0
+    # plan (header, prefix sums, first sequence of each of up to 2048 ranges,
+    # 256-byte aligned) + (B + 2048) partials of 8 heads x (64 + 2) floats per kv head
+    B, hkv = 512, 8
+    plan = ((4 + B + 1 + 2048) * 4 + 255) // 256 * 256
+    assert gkv.workspace_bytes(B, hkv, 2049) == plan + (B + 2048) * hkv * (512 + 16) * 4
+    assert gkv.workspace_bytes(B, hkv, 2049) == gkv.workspace_bytes(B, hkv, 9, window=128)
