@@ -9,25 +9,29 @@
 // (getp-csrc/kernels/fast_attention.hpp:566-622) and its in-workgroup merge
 // (:383-424) with a paged, variable-length, token-balanced design.
 //
-// Work split (three launches).
-//   plan     one workgroup: prefix sums of the sequences' token counts, each
-//            padded to a multiple of 32, into `cu`; the total T is cut into
-//            equal ranges of S tokens, one per split workgroup, and the first
-//            sequence of each range is recorded. Lengths vary from 1 to
-//            thousands of tokens; equal ranges keep every workgroup equally
-//            busy, with as many workgroups as the GPU holds at once.
-//   split    workgroup w owns tokens [w*S, (w+1)*S) of the concatenated
-//            sequences, which can span several sequences (segments). Wave g
-//            works on kv head g, so the workgroup's waves stream the H_kv
-//            contiguous 2 KB head slices of each block together; each K/V byte
-//            is read once for all G query heads of its group. A segment that
-//            is a whole sequence is finished in place (sink added, output
-//            written); a piece of a longer sequence leaves (m, l, o) partials
-//            in the workspace at index b + w (unique: ranges are contiguous).
-//            Waves raise their issue priority while they have more of their
-//            range left, so that co-resident workgroups advance together
-//            instead of the oldest waves running first and the others alone
-//            at the end.
+// Three launches.
+//   prep     Lays all sequences end to end in one token stream, each padded
+//            to whole steps of 32 tokens (prefix sums `cu`), and cuts the
+//            stream into equal ranges of S tokens, one per split workgroup
+//            (as many as the GPU holds at once). For every 16-token block of
+//            the stream it records the physical block id (checked against the
+//            pool) and for every step its sequence, how many of its tokens
+//            exist, and whether it is the sequence's first or last step. It
+//            also prepares each (sequence, kv head)'s query operands: RoPE at
+//            the sequence's last position, the 1/8 scale and log2(e), split
+//            into bf16 high and low pieces, in the register layout of the
+//            matrix-core operand.
+//   split    Workgroup w streams steps [w*S, (w+1)*S)/32 of the stream for
+//            every kv head, one wave per SIMD (wave i takes heads i, i+4, ...).
+//            A range spans several sequences and the loads never stop at a
+//            sequence boundary: each step's block ids and step record come
+//            from registers loaded once per range, and its query operands
+//            travel in the load ring with its K and V; at a boundary only the
+//            softmax state is flushed. Each K/V byte is read once for all G
+//            query heads of its group. A sequence inside one range is
+//            finished in place (sink added, output written); a piece of a
+//            longer sequence leaves (m, l, o) partials in the workspace at
+//            index b + w (unique: ranges are contiguous).
 //   combine  one workgroup per sequence split over several ranges: merges the
 //            partials with the sink; writes zeros for empty sequences.
 //
@@ -44,10 +48,12 @@
 //   register transposes, no LDS.
 //
 // Memory: raw buffer loads, one block of one head per instruction (scalar
-// base, constant per-lane offset, 2 KB range); R - 1 steps (8 KB each) of
-// every wave in flight. Every load is unconditional (indices are clamped), so
-// the compiler's wait counts are exact and a step never waits for the
-// prefetches issued after it.
+// base, constant per-lane offset, 2 KB range); R - 1 steps (8 KB of K/V
+// each) in flight per wave, held in VGPRs and AGPRs (one wave per SIMD: two
+// waves on a SIMD are not served equally, the older one issues first, which
+// leaves the younger ones running alone at the end). Every load is
+// unconditional (indices are clamped), so the compiler's wait counts are
+// exact and a step never waits for the prefetches issued after it.
 #include "gkv_device.hpp"
 
 #include <algorithm>
@@ -61,8 +67,20 @@ constexpr int kMlStride = 16;          // floats of (m, l) per partial: 8 heads 
 constexpr int kPartFloats = kCols * kHeadDim;
 constexpr int kMaxWorkgroups = 2048;   // split workgroups per launch (workspace bound)
 constexpr int kPlanHeader = 4;         // ints: T, S, workgroups used, unused
-constexpr int kIdRegs = 4;             // block-id registers per wave: segments of <= 4096 tokens
+constexpr int kIdRegs = 4;             // block-id registers per wave: ranges of <= 4096 tokens
 constexpr int kMaxRange = kIdRegs * 64 * kBlockTokens;
+constexpr int kInfoRegs = kMaxRange / kStep / 64; // step-record registers
+constexpr int kSplitThreads = 256;     // split kernel: 4 waves, one per SIMD
+constexpr int kPrepThreads = 1024;
+constexpr int kMaxBatch = 8192;        // sequences per call (prefix sums kept in LDS)
+constexpr int kBadBlock = -1;          // F entry: id outside the pool
+constexpr int kPadBlock = -2;          // F entry: no tokens (padding)
+
+// Step record: sequence << 8 | first step of the sequence << 7 | its last
+// step << 6 | tokens of the step that exist (0..32).
+__host__ __device__ constexpr int step_record(int b, bool first, bool last, int valid) {
+  return (b << 8) | (first ? 0x80 : 0) | (last ? 0x40 : 0) | valid;
+}
 
 struct DecodeArgs {
   const float *q;
@@ -78,8 +96,10 @@ struct DecodeArgs {
   int B;
   int n_wg;           // split workgroups launched
   int fixed_S;        // 0: S = T / n_wg (balanced); > 0: this S
-  int prio;           // 1: waves raise their priority while behind
-  int32_t *plan;      // [kPlanHeader][cu: B + 1][first sequence per workgroup: n_wg]
+  int32_t *plan;      // [kPlanHeader][cu: B + 1]
+  int32_t *flat;      // block id of every 16-token block of the stream
+  int32_t *steps;     // step record of every 32-token step of the stream
+  u32x4 *qops;        // [B][Hkv][64 lanes][2]: query operands
   float *ws_o;        // [B + kMaxWorkgroups][Hkv][8][64]
   float *ws_ml;       // [B + kMaxWorkgroups][Hkv][8][2]
   void *out;
@@ -119,33 +139,58 @@ __device__ __forceinline__ bf16x8 pack_pieces(const float (&x)[8], bool lo) {
   return r;
 }
 
-// Wave issue priority 0..3 (s_setprio takes an immediate).
-__device__ __forceinline__ void set_priority(int p) {
-  switch (p) {
-  case 3:
-    __builtin_amdgcn_s_setprio(3);
-    break;
-  case 2:
-    __builtin_amdgcn_s_setprio(2);
-    break;
-  case 1:
-    __builtin_amdgcn_s_setprio(1);
-    break;
-  default:
-    __builtin_amdgcn_s_setprio(0);
+// ---- prep -----------------------------------------------------------------------
+
+// Query operands of sequence b, kv head g, for one wave. Lane (kg = lane/16,
+// col): column col is query head g*G + (col & 7) (zero past G), the high bf16
+// piece for col < 8, the low piece for col >= 8; operand 0 holds dims
+// 8kg .. 8kg+7, operand 1 dims 32 + 8kg .. +7 (the two halves of each RoPE
+// pair sit in the same lane).
+__device__ void prep_queries(const DecodeArgs &a, int item) {
+  constexpr int D = kHeadDim;
+  const int b = item / a.n_kv_heads, g = item - b * a.n_kv_heads;
+  const int lane = threadIdx.x & 63, col = lane & 15, kg = lane >> 4;
+  const bool lo = col >= 8;
+  const int head = col & 7;
+  const bool head_ok = head < a.G;
+  const int hq = g * a.G + (head_ok ? head : 0);
+  const float *qp = a.q + (int64_t)b * a.q_stride + hq * D + 8 * kg;
+  float qa[8], qb[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    qa[i] = qp[i];
+    qb[i] = qp[32 + i];
   }
+  if (a.cos_tab) {
+    const int pos = max(a.seq_lens[b] - 1, 0);
+    const float *cp = a.cos_tab + (int64_t)pos * (D / 2) + 8 * kg;
+    const float *sp = a.sin_tab + (int64_t)pos * (D / 2) + 8 * kg;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float x1 = qa[i], x2 = qb[i], c = cp[i], s = sp[i];
+      qa[i] = rope_first(x1, x2, c, s);
+      qb[i] = rope_second(x1, x2, c, s);
+    }
+  }
+  const float qscale = head_ok ? 0.125f * kLog2e : 0.0f; // 1/sqrt(64); exp -> exp2
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    qa[i] *= qscale;
+    qb[i] *= qscale;
+  }
+  u32x4 *dst = a.qops + ((int64_t)item * 64 + lane) * 2;
+  dst[0] = __builtin_bit_cast(u32x4, pack_pieces(qa, lo));
+  dst[1] = __builtin_bit_cast(u32x4, pack_pieces(qb, lo));
 }
 
-// ---- plan ---------------------------------------------------------------------
-
-constexpr int kPlanThreads = 1024;
-
-__global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(DecodeArgs a) {
-  __shared__ int s_scan[2][kPlanThreads];
-  __shared__ int s_total;
+// Every workgroup computes the prefix sums in LDS (the lengths are 4 bytes per
+// sequence, cheap to read again), then takes its share of the stream blocks
+// and of the query items; workgroup 0 also publishes the plan.
+__global__ __launch_bounds__(kPrepThreads) void decode_prep_kernel(DecodeArgs a) {
+  __shared__ int s_cu[kMaxBatch + 1];
+  __shared__ int s_scan[2][kPrepThreads];
   const int t = threadIdx.x, B = a.B;
-  int32_t *cu = a.plan + kPlanHeader, *first = cu + B + 1;
-  const int per = (B + kPlanThreads - 1) / kPlanThreads;
+  const int per = (B + kPrepThreads - 1) / kPrepThreads;
   const int b0 = t * per;
   int local = 0;
   bool any_over = false;
@@ -157,13 +202,13 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(DecodeArgs a)
       any_over |= over;
     }
   }
-  if (any_over && a.dev_err)
+  if (any_over && blockIdx.x == 0 && a.dev_err)
     atomicOr(a.dev_err, GKV_DEVERR_LENGTH);
   // inclusive scan of the per-thread sums (Hillis-Steele, double buffered)
   int buf = 0;
   s_scan[0][t] = local;
   __syncthreads();
-  for (int off = 1; off < kPlanThreads; off <<= 1) {
+  for (int off = 1; off < kPrepThreads; off <<= 1) {
     const int v = s_scan[buf][t] + (t >= off ? s_scan[buf][t - off] : 0);
     s_scan[buf ^ 1][t] = v;
     buf ^= 1;
@@ -173,36 +218,65 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(DecodeArgs a)
   for (int i = 0; i < per; i++) {
     const int b = b0 + i;
     if (b < B) {
-      cu[b] = run;
+      s_cu[b] = run;
       run += pad_step(seq_tokens(a, b));
     }
   }
-  if (t == kPlanThreads - 1) {
-    s_total = s_scan[buf][t];
-    cu[B] = s_total;
-  }
-  // Every range starts as "no sequence" (B); then each sequence claims the
-  // ranges whose first token it holds.
-  for (int w = t; w < a.n_wg; w += kPlanThreads)
-    first[w] = B;
+  if (t == kPrepThreads - 1)
+    s_cu[B] = s_scan[buf][t];
   __syncthreads();
-  const int T = s_total;
+  const int T = s_cu[B];
   int S = a.fixed_S;
   if (S == 0)
     S = max(kStep, pad_step((T + a.n_wg - 1) / a.n_wg));
-  for (int i = 0; i < per; i++) {
-    const int b = b0 + i;
-    if (b < B) {
-      const int c0 = cu[b], c1 = cu[b + 1];
-      for (int w = (c0 + S - 1) / S; w * S < c1 && w < a.n_wg; w++)
-        first[w] = b;
+  if (blockIdx.x == 0) {
+    int32_t *cu = a.plan + kPlanHeader;
+    for (int b = t; b <= B; b += kPrepThreads)
+      cu[b] = s_cu[b];
+    if (t == 0) {
+      a.plan[0] = T;
+      a.plan[1] = S;
+      a.plan[2] = min(a.n_wg, (T + S - 1) / S);
     }
   }
-  if (t == 0) {
-    a.plan[0] = T;
-    a.plan[1] = S;
-    a.plan[2] = min(a.n_wg, (T + S - 1) / S);
+
+  // Stream blocks (and the step records at even blocks), grid-strided.
+  bool any_bad = false;
+  const int n_e = T / kBlockTokens;
+  for (int e = blockIdx.x * kPrepThreads + t; e < n_e; e += gridDim.x * kPrepThreads) {
+    const int tok = e * kBlockTokens;
+    int lo = 0, hi = B - 1; // the sequence holding the block: last b with cu[b] <= tok
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_cu[mid] <= tok)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    const int b = lo;
+    const int off = tok - s_cu[b];
+    const int n = seq_tokens(a, b);
+    int id = kPadBlock;
+    if (off < n) {
+      id = a.table[(int64_t)b * a.table_stride + off / kBlockTokens];
+      if (id < 0 || id >= a.num_blocks) {
+        id = kBadBlock;
+        any_bad = true;
+      }
+    }
+    a.flat[e] = id;
+    if ((e & 1) == 0)
+      a.steps[e >> 1] = step_record(b, off == 0, tok + kStep == s_cu[b + 1],
+                                    min(max(n - off, 0), kStep));
   }
+  if (any_bad && a.dev_err)
+    atomicOr(a.dev_err, GKV_DEVERR_BLOCK_ID);
+
+  // Query operands: one wave per (sequence, kv head).
+  const int waves = kPrepThreads / 64;
+  for (int item = blockIdx.x * waves + (t >> 6); item < B * a.n_kv_heads;
+       item += gridDim.x * waves)
+    prep_queries(a, item);
 }
 
 // ---- split ----------------------------------------------------------------------
@@ -210,7 +284,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(DecodeArgs a)
 // R: depth of the register ring of loaded steps (R - 1 steps in flight ahead
 // of the one being computed).
 template <int R>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(R == 2 ? 4 : (R == 3 ? 3 : 2))))
+__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(1)))
 void decode_split_kernel(DecodeArgs a) {
   constexpr int D = kHeadDim;
   const int w_id = blockIdx.x;
@@ -219,87 +293,55 @@ void decode_split_kernel(DecodeArgs a) {
   if (rs >= T)
     return;
   const int re = min(rs + S, T);
-  const int32_t *cu = a.plan + kPlanHeader;
-  const int first_b = a.plan[kPlanHeader + a.B + 1 + w_id];
+  const int n_steps = (re - rs) / kStep; // every sequence is padded to whole steps
 
   const int lane = threadIdx.x & 63;
-  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // wave-uniform: kv head
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // wave-uniform
+  const int n_waves = blockDim.x >> 6;
   const int col = lane & 15, kg = lane >> 4;
   const bool lo = col >= 8;
   const int head = col & 7;
   const bool head_ok = head < a.G;
-  const int hq = g * a.G + head;
-  const int hq_c = head_ok ? hq : g * a.G; // a valid head for the padding columns
 
   // Per-lane load offsets (bytes), the same for every step.
   const uint32_t k_off = (uint32_t)(col * D + 8 * kg) * 2;
   const uint32_t v_off = (uint32_t)(col * kBlockTokens + 4 * kg) * 2; // + nn * 512
   const size_t head_bytes = (size_t)kBlockTokens * D * 2;               // 2 KB
 
-  if (a.prio)
-    if (a.prio)
-    set_priority(3);
-
-  // Block ids, up to kIdRegs * 64 per segment, one per lane per register:
-  // loaded for the first segment here and for each next segment while the
-  // current one streams, so a segment never starts with a dependent table
-  // load. Rows are read with clamped indices (always inside the table).
-  auto load_ids = [&](int bb, int blk0, int (&ids)[kIdRegs]) {
-    const int32_t *row = a.table + (int64_t)bb * a.table_stride;
+  // Block ids and step records of the range, one per lane per register.
+  const int e0 = rs / kBlockTokens, s0 = rs / kStep;
+  int tv[kIdRegs], ti[kInfoRegs];
 #pragma unroll
-    for (int i = 0; i < kIdRegs; i++)
-      ids[i] = row[min(blk0 + 64 * i + lane, a.table_stride - 1)];
+  for (int i = 0; i < kIdRegs; i++)
+    tv[i] = a.flat[e0 + min(64 * i + lane, 2 * n_steps - 1)];
+#pragma unroll
+  for (int i = 0; i < kInfoRegs; i++)
+    ti[i] = a.steps[s0 + min(64 * i + lane, n_steps - 1)];
+
+  auto pick = [&](const int *regs, int nregs, int j) -> int {
+    const int w = j >> 6, l = j & 63;
+    int v = __builtin_amdgcn_readlane(regs[0], l);
+    for (int i = 1; i < nregs; i++)
+      if (w == i)
+        v = __builtin_amdgcn_readlane(regs[i], l);
+    return v;
   };
-  int tv[kIdRegs];
-  load_ids(min(first_b, a.B - 1), max(rs - cu[min(first_b, a.B - 1)], 0) / kBlockTokens, tv);
 
-  for (int b = first_b; b < a.B; b++) {
-    const int c0 = cu[b], c1 = cu[b + 1];
-    if (c0 >= re)
-      break;
-    // ids of the segment after this one (the next sequence from its start)
-    int tvn[kIdRegs];
-    load_ids(min(b + 1, a.B - 1), 0, tvn);
-    if (c1 == c0) { // empty sequence: the combine writes its zeros
-#pragma unroll
-      for (int i = 0; i < kIdRegs; i++)
-        tv[i] = tvn[i];
-      continue;
-    }
-    const int n = seq_tokens(a, b);
-    const int t_begin = max(rs, c0) - c0;         // multiple of 32
-    const int t_end = min(min(re, c1) - c0, n);   // real tokens of this segment end here
-    const bool complete = rs <= c0 && c1 <= re;
-    const int n_tok = max(t_end - t_begin, 0);
-    const int n_steps = (n_tok + kStep - 1) / kStep;
-    const int n_blk = (n_tok + kBlockTokens - 1) / kBlockTokens;
-    const int L = a.seq_lens[b];
-    const int seg0 = c0 + t_begin - rs; // tokens of the range before this segment
-    uint32_t seg_bad = 0;               // a bad block id met in this segment
-
-    // Block id j of the segment (j < n_blk <= 64 * kIdRegs); ids outside the
-    // pool read block 0 and set bit (j & 1) of `bad`.
-    auto block_id = [&](int j, uint32_t &bad) -> int {
-      const int w = j >> 6, l = j & 63;
-      int v = __builtin_amdgcn_readlane(tv[0], l);
-#pragma unroll
-      for (int i = 1; i < kIdRegs; i++)
-        if (w == i)
-          v = __builtin_amdgcn_readlane(tv[i], l);
-      if (v < 0 || v >= a.num_blocks) {
-        bad |= 1u << (j & 1);
-        v = 0;
-      }
-      return v;
-    };
-
-    u32x4 kbuf[R][4], vbuf[R][4];
-    uint32_t bad_ring[R];
-    auto load_step = [&](int step, u32x4 (&kr)[4], u32x4 (&vr)[4], uint32_t &bad) {
-      const int j0 = 2 * step;
-      bad = 0;
-      const int p0 = block_id(j0, bad);
-      const int p1 = j0 + 1 < n_blk ? block_id(j0 + 1, bad) : p0;
+  // One wave per SIMD; wave wv works on kv heads wv, wv + n_waves, ... in
+  // turn, each over the whole range.
+  for (int g = wv; g < a.n_kv_heads; g += n_waves) {
+    // Ring slot: K (4 x 16 B per lane), V (4 x 16 B), the step's query
+    // operands (2 x 16 B), and its record with the bad-block bits.
+    u32x4 kbuf[R][4], vbuf[R][4], qbuf[R][2];
+    int rec[R], badb[R];
+    auto load_step = [&](int step, u32x4 (&kr)[4], u32x4 (&vr)[4], u32x4 (&qr)[2], int &rc,
+                         int &bb) {
+      int p0 = pick(tv, kIdRegs, 2 * step), p1 = pick(tv, kIdRegs, 2 * step + 1);
+      rc = pick(ti, kInfoRegs, step);
+      // a bad id masks its block like padding (bit jt per block)
+      bb = (p0 == kBadBlock ? 1 : 0) | (p1 == kBadBlock ? 2 : 0);
+      p0 = max(p0, 0);
+      p1 = max(p1, 0);
       const size_t h0 = ((size_t)p0 * a.n_kv_heads + g) * head_bytes;
       const size_t h1 = ((size_t)p1 * a.n_kv_heads + g) * head_bytes;
       const __amdgpu_buffer_rsrc_t k0 = head_rsrc((const char *)a.kc + h0);
@@ -316,60 +358,93 @@ void decode_split_kernel(DecodeArgs a) {
         const u32x2 y = __builtin_amdgcn_raw_buffer_load_b64(v1, v_off + nn * 512, 0, 0);
         vr[nn] = u32x4{x[0], x[1], y[0], y[1]};
       }
+      const u32x4 *qs = a.qops + (((int64_t)(rc >> 8) * a.n_kv_heads + g) * 64 + lane) * 2;
+      qr[0] = qs[0];
+      qr[1] = qs[1];
     };
 
-    // First loads out before the query work, so their latency overlaps it.
-    // Every load is unconditional (indices clamped): the compiler's wait
-    // counts are then exact, and a step never waits for later prefetches.
-    const int last_step = max(n_steps - 1, 0);
+    // The ring's first loads go out before anything else.
+    const int last_step = n_steps - 1;
 #pragma unroll
     for (int r = 0; r < R - 1; r++)
-      load_step(min(r, last_step), kbuf[r], vbuf[r], bad_ring[r]);
+      load_step(min(r, last_step), kbuf[r], vbuf[r], qbuf[r], rec[r], badb[r]);
 
-    // Query: dims 8*kg + i (first MFMA) and 32 + 8*kg + i (second); the two
-    // halves of a RoPE pair sit in the same lane.
-    float qa[8], qb[8];
-    {
-      const float *qp = a.q + (int64_t)b * a.q_stride + hq_c * D + 8 * kg;
-      const float4 x0 = *(const float4 *)(qp), x1 = *(const float4 *)(qp + 4);
-      const float4 y0 = *(const float4 *)(qp + 32), y1 = *(const float4 *)(qp + 36);
-      qa[0] = x0.x; qa[1] = x0.y; qa[2] = x0.z; qa[3] = x0.w;
-      qa[4] = x1.x; qa[5] = x1.y; qa[6] = x1.z; qa[7] = x1.w;
-      qb[0] = y0.x; qb[1] = y0.y; qb[2] = y0.z; qb[3] = y0.w;
-      qb[4] = y1.x; qb[5] = y1.y; qb[6] = y1.z; qb[7] = y1.w;
-      if (a.cos_tab) {
-        const int pos = max(L - 1, 0);
-        const float *cp = a.cos_tab + (int64_t)pos * (D / 2) + 8 * kg;
-        const float *sp = a.sin_tab + (int64_t)pos * (D / 2) + 8 * kg;
-        const float4 cc0 = *(const float4 *)cp, cc1 = *(const float4 *)(cp + 4);
-        const float4 ss0 = *(const float4 *)sp, ss1 = *(const float4 *)(sp + 4);
-        const float cv[8] = {cc0.x, cc0.y, cc0.z, cc0.w, cc1.x, cc1.y, cc1.z, cc1.w};
-        const float sv[8] = {ss0.x, ss0.y, ss0.z, ss0.w, ss1.x, ss1.y, ss1.z, ss1.w};
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const float x1v = qa[i], x2v = qb[i];
-          qa[i] = rope_first(x1v, x2v, cv[i], sv[i]);
-          qb[i] = rope_second(x1v, x2v, cv[i], sv[i]);
-        }
-      }
-      const float qscale = head_ok ? 0.125f * kLog2e : 0.0f; // 1/sqrt(64); exp -> exp2
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        qa[i] *= qscale;
-        qb[i] *= qscale;
-      }
-    }
-    const bf16x8 qop0 = pack_pieces(qa, lo), qop1 = pack_pieces(qb, lo);
-
-    const float sink2 = head_ok ? a.sinks[hq_c] * kLog2e : 0.0f;
-    float m_run = sink2; // running reference max (log2 units) of this column
+    const float sink2 = head_ok ? a.sinks[g * a.G + head] * kLog2e : 0.0f;
+    int cur_b = -1;             // sequence of the open segment (-1: none)
+    bool cur_whole = false;     // the segment began at its sequence's first step
+    bool cur_ends = false;      // ... and has reached its last step
+    float m_run = sink2;        // running reference max (log2 units) of this column
     float lsum = 0.0f;
     f32x4 o[4];
 #pragma unroll
     for (int nn = 0; nn < 4; nn++)
       o[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto compute_step = [&](int step, u32x4 (&kr)[4], u32x4 (&vr)[4], uint32_t bad) {
+    // Finishes the open segment: the output (sink added) if it is the whole
+    // sequence, else the partial for the combine.
+    auto flush = [&]() {
+      float ls = lsum;
+      ls += __shfl_xor(ls, 16);
+      ls += __shfl_xor(ls, 32);
+      f32x4 oo[4];
+#pragma unroll
+      for (int nn = 0; nn < 4; nn++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          oo[nn][r] = o[nn][r] + swap8(o[nn][r]);
+      if (lo || !head_ok || cur_b < 0)
+        return;
+      const int hq = g * a.G + head;
+      if (cur_whole && cur_ends) {
+        // out = o * 2^(m - M) / (l * 2^(m - M) + 2^(sink - M)), M = max(m, sink)
+        const float M2 = fmaxf(m_run, sink2);
+        const float f = __builtin_amdgcn_exp2f(m_run - M2);
+        const float scale = f / fmaf(ls, f, __builtin_amdgcn_exp2f(sink2 - M2));
+        const int64_t ob = (int64_t)cur_b * a.out_stride + (int64_t)hq * D + 4 * kg;
+#pragma unroll
+        for (int nn = 0; nn < 4; nn++) {
+          if (a.out_bf16) {
+            typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+            *(bf16x4 *)((__bf16 *)a.out + ob + 16 * nn) =
+                bf16x4{(__bf16)(oo[nn][0] * scale), (__bf16)(oo[nn][1] * scale),
+                       (__bf16)(oo[nn][2] * scale), (__bf16)(oo[nn][3] * scale)};
+          } else {
+            *(f32x4 *)((float *)a.out + ob + 16 * nn) = oo[nn] * scale;
+          }
+        }
+      } else {
+        const int64_t part = ((int64_t)(cur_b + w_id)) * a.n_kv_heads + g;
+        float *wo = a.ws_o + part * kPartFloats + head * D + 4 * kg;
+#pragma unroll
+        for (int nn = 0; nn < 4; nn++)
+          *(f32x4 *)(wo + 16 * nn) = oo[nn];
+        if (kg == 0) {
+          a.ws_ml[part * kMlStride + 2 * head] = m_run;
+          a.ws_ml[part * kMlStride + 2 * head + 1] = ls;
+        }
+      }
+    };
+
+    auto compute_step = [&](u32x4 (&kr)[4], u32x4 (&vr)[4], u32x4 (&qr)[2], int rc, int bb,
+                            bool in_range) {
+      const int sb = rc >> 8;
+      if (in_range && sb != cur_b) {
+        // The step starts another sequence: flush, start a new segment.
+        flush();
+        cur_b = sb;
+        cur_whole = (rc & 0x80) != 0;
+        m_run = sink2;
+        lsum = 0.0f;
+#pragma unroll
+        for (int nn = 0; nn < 4; nn++)
+          o[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      if (in_range)
+        cur_ends = (rc & 0x40) != 0;
+      const int valid = in_range ? (rc & 0x3f) : 0;
+      const uint32_t bad = (uint32_t)bb;
+      const bf16x8 qop0 = __builtin_bit_cast(bf16x8, qr[0]);
+      const bf16x8 qop1 = __builtin_bit_cast(bf16x8, qr[1]);
       // Scores of token 4*kg + r of block jt (slot 4*jt + r), this lane's column.
       float sc[8];
 #pragma unroll
@@ -383,10 +458,10 @@ void decode_split_kernel(DecodeArgs a) {
         for (int r = 0; r < 4; r++)
           sc[4 * jt + r] = acc[r] + swap8(acc[r]);
       }
-      const int valid = min(kStep, n_tok - step * kStep);
       if (valid < kStep || bad) {
-        // Tail of the sequence, padding, or a bad block id: those tokens get
-        // weight 0 and their values (possibly never written) become zeros.
+        // Tail of the sequence, padding, past the range, or a bad block id:
+        // those tokens get weight 0 and their values (possibly never written)
+        // become zeros.
 #pragma unroll
         for (int jt = 0; jt < 2; jt++) {
           const bool blk_bad = (bad >> jt) & 1;
@@ -396,10 +471,10 @@ void decode_split_kernel(DecodeArgs a) {
               sc[4 * jt + r] = -INFINITY;
 #pragma unroll
           for (int h2 = 0; h2 < 2; h2++) {
-            const int t = 16 * jt + 4 * kg + 2 * h2;
+            const int tk = 16 * jt + 4 * kg + 2 * h2;
             const uint32_t keep = blk_bad ? 0u
-                                          : ((t < valid ? 0x0000ffffu : 0u) |
-                                             (t + 1 < valid ? 0xffff0000u : 0u));
+                                          : ((tk < valid ? 0x0000ffffu : 0u) |
+                                             (tk + 1 < valid ? 0xffff0000u : 0u));
 #pragma unroll
             for (int nn = 0; nn < 4; nn++)
               vr[nn][2 * jt + h2] &= keep;
@@ -440,65 +515,19 @@ void decode_split_kernel(DecodeArgs a) {
 
     // Ring: slot r holds step base + r; the load for step + R - 1 goes out
     // before step is computed. The step count is padded to a multiple of R;
-    // padded steps re-load the last step (cache hits) and are fully masked.
+    // padded steps re-load the last step (cache hits) and are masked out.
     for (int base = 0; base < n_steps; base += R) {
-      // priority from the share of the range still ahead of this wave
-      if (a.prio)
-        set_priority((4 * (S - seg0 - base * kStep) - 1) / S);
 #pragma unroll
       for (int r = 0; r < R; r++) {
         const int step = base + r;
         const int slot = (r + R - 1) % R;
-        load_step(min(step + R - 1, last_step), kbuf[slot], vbuf[slot], bad_ring[slot]);
-        seg_bad |= bad_ring[slot];
-        compute_step(step, kbuf[r], vbuf[r], bad_ring[r]);
+        load_step(min(step + R - 1, last_step), kbuf[slot], vbuf[slot], qbuf[slot], rec[slot],
+                  badb[slot]);
+        compute_step(kbuf[r], vbuf[r], qbuf[r], rec[r], badb[r], step < n_steps);
       }
     }
-    if (seg_bad && lane == 0 && a.dev_err)
-      atomicOr(a.dev_err, GKV_DEVERR_BLOCK_ID);
-#pragma unroll
-    for (int i = 0; i < kIdRegs; i++)
-      tv[i] = tvn[i];
-
-    // Wave totals: sum over the 4 k-groups; the lo column adds its part of O.
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
-#pragma unroll
-    for (int nn = 0; nn < 4; nn++)
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        o[nn][r] += swap8(o[nn][r]);
-    if (lo || !head_ok)
-      continue;
-    if (complete) {
-      // out = o * 2^(m - M) / (l * 2^(m - M) + 2^(sink - M)), M = max(m, sink)
-      const float M2 = fmaxf(m_run, sink2);
-      const float f = __builtin_amdgcn_exp2f(m_run - M2);
-      const float scale = f / fmaf(lsum, f, __builtin_amdgcn_exp2f(sink2 - M2));
-      const int64_t ob = (int64_t)b * a.out_stride + (int64_t)hq * D + 4 * kg;
-#pragma unroll
-      for (int nn = 0; nn < 4; nn++) {
-        if (a.out_bf16) {
-          typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-          *(bf16x4 *)((__bf16 *)a.out + ob + 16 * nn) =
-              bf16x4{(__bf16)(o[nn][0] * scale), (__bf16)(o[nn][1] * scale),
-                     (__bf16)(o[nn][2] * scale), (__bf16)(o[nn][3] * scale)};
-        } else {
-          *(f32x4 *)((float *)a.out + ob + 16 * nn) = o[nn] * scale;
-        }
-      }
-    } else {
-      const int64_t part = ((int64_t)(b + w_id)) * a.n_kv_heads + g;
-      float *wo = a.ws_o + part * kPartFloats + head * D + 4 * kg;
-#pragma unroll
-      for (int nn = 0; nn < 4; nn++)
-        *(f32x4 *)(wo + 16 * nn) = o[nn];
-      if (kg == 0) {
-        a.ws_ml[part * kMlStride + 2 * head] = m_run;
-        a.ws_ml[part * kMlStride + 2 * head + 1] = lsum;
-      }
-    }
-  }
+    flush();
+  } // kv heads
 }
 
 // ---- combine --------------------------------------------------------------------
@@ -549,38 +578,40 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
 
 // ---- host side --------------------------------------------------------------------
 
-constexpr int kRing = 4;
+constexpr int kRing = 5;
 
 // Ring depth of the split kernel (default kRing; the tuning variable
-// GKV_DECODE_RING = 2..4 picks another, read once).
+// GKV_DECODE_RING = 4..8 picks another, read once).
 static int ring_depth() {
   static const int r = [] {
     const char *e = getenv("GKV_DECODE_RING");
     const int v = e ? atoi(e) : kRing;
-    return (v >= 2 && v <= 4) ? v : kRing;
+    return (v >= 4 && v <= 8) ? v : kRing;
   }();
   return r;
 }
 
-// Wave priority balancing (default on; GKV_DECODE_PRIO=0 switches it off).
-static int prio_enabled() {
-  static const int p = [] {
-    const char *e = getenv("GKV_DECODE_PRIO");
-    return e ? (atoi(e) != 0) : 1;
-  }();
-  return p;
+template <int R>
+static void launch_split_ring(const DecodeArgs &a, dim3 grid, dim3 block, hipStream_t s) {
+  hipLaunchKernelGGL(decode_split_kernel<R>, grid, block, 0, s, a);
 }
 
 static const void *split_kernel_fn(int ring) {
   switch (ring) {
-  case 3:
-    return (const void *)decode_split_kernel<3>;
   case 4:
     return (const void *)decode_split_kernel<4>;
+  case 6:
+    return (const void *)decode_split_kernel<6>;
+  case 7:
+    return (const void *)decode_split_kernel<7>;
+  case 8:
+    return (const void *)decode_split_kernel<8>;
   default:
-    return (const void *)decode_split_kernel<2>;
+    return (const void *)decode_split_kernel<5>;
   }
 }
+
+static int split_block(int n_kv_heads) { return 64 * std::min(4, n_kv_heads); }
 
 // Workgroups the GPU holds at once for the split kernel (CUs x per-CU
 // occupancy), per device, measured once.
@@ -594,20 +625,37 @@ static int resident_workgroups(int n_kv_heads) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, split_kernel_fn(ring_depth()),
-                                                     64 * n_kv_heads, 0) != hipSuccess)
+                                                     split_block(n_kv_heads), 0) != hipSuccess)
       return 0;
     slot = std::max(1, cus * per_cu);
   }
   return slot;
 }
 
-static size_t plan_bytes(int B) {
-  return ((size_t)(kPlanHeader + B + 1 + kMaxWorkgroups) * 4 + 255) & ~(size_t)255;
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Workspace layout: plan | block ids | step records | query operands |
+// partials (o) | partials (m, l).
+struct WorkspaceLayout {
+  size_t plan, flat, steps, qops, ws_o, ws_ml, total;
+};
+
+static WorkspaceLayout layout_of(int B, int n_kv_heads, int64_t t_max) {
+  WorkspaceLayout L;
+  L.plan = 0;
+  L.flat = align256((size_t)(kPlanHeader + B + 1) * 4);
+  L.steps = L.flat + align256((size_t)(t_max / kBlockTokens + 1) * 4);
+  L.qops = L.steps + align256((size_t)(t_max / kStep + 1) * 4);
+  L.ws_o = L.qops + align256((size_t)B * n_kv_heads * 64 * 32);
+  const size_t parts = (size_t)(B + kMaxWorkgroups) * n_kv_heads;
+  L.ws_ml = L.ws_o + parts * kPartFloats * sizeof(float);
+  L.total = L.ws_ml + parts * kMlStride * sizeof(float);
+  return L;
 }
 
-static size_t workspace_bytes(int B, int n_kv_heads) {
-  const size_t parts = (size_t)(B + kMaxWorkgroups) * n_kv_heads;
-  return plan_bytes(B) + parts * (kPartFloats + kMlStride) * sizeof(float);
+static int64_t stream_max(int32_t B, int32_t max_seq_len, int32_t window) {
+  const int64_t n_max = window > 0 ? std::min(max_seq_len, window) : max_seq_len;
+  return (int64_t)B * ((n_max + kStep - 1) / kStep * kStep);
 }
 
 static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, int64_t q_stride,
@@ -624,8 +672,8 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
     return GKV_ERR_ARG;
   if (n_q_heads % cache.n_kv_heads != 0)
     return GKV_ERR_ARG;
-  if (cache.n_kv_heads > 8)
-    return GKV_ERR_UNSUPPORTED; // one wave per kv head, 512 threads
+  if (cache.n_kv_heads > 8 || B > kMaxBatch)
+    return GKV_ERR_UNSUPPORTED; // combine: one wave per kv head; prep: prefix sums in LDS
   const int G = n_q_heads / cache.n_kv_heads;
   if (G > kCols)
     return GKV_ERR_UNSUPPORTED;
@@ -639,27 +687,30 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
     return GKV_ERR_ARG;
   if (cache.ring > 0 && window == 0)
     return GKV_ERR_ARG; // a ring holds only the last W tokens
-  const int64_t n_max = window > 0 ? std::min(max_seq_len, window) : max_seq_len;
-  const int64_t t_max = (int64_t)B * ((n_max + kStep - 1) / kStep * kStep);
-  if (t_max >= INT32_MAX)
+  const int64_t t_max = stream_max(B, max_seq_len, window);
+  if (t_max >= (1 << 30) || (int64_t)B << 8 >= INT32_MAX)
     return GKV_ERR_ARG;
-  if (!workspace || workspace_bytes_given < workspace_bytes(B, cache.n_kv_heads))
-    return GKV_ERR_WORKSPACE;
   // Ranges hold at most kMaxRange tokens (the block ids a wave keeps).
   const int64_t min_wg = (t_max + kMaxRange - 1) / kMaxRange;
-  int64_t n_wg;
+  int64_t n_wg = 0;
   if (split_tokens > 0) {
     if (split_tokens > kMaxRange)
       return GKV_ERR_ARG;
     n_wg = std::max<int64_t>(1, (t_max + split_tokens - 1) / split_tokens);
-  } else {
+    if (n_wg > kMaxWorkgroups)
+      return GKV_ERR_ARG;
+  }
+  const WorkspaceLayout L = layout_of(B, cache.n_kv_heads, t_max);
+  if (!workspace || workspace_bytes_given < L.total)
+    return GKV_ERR_WORKSPACE;
+  if (split_tokens == 0) {
     const int resident = (need_cache && B > 0) ? resident_workgroups(cache.n_kv_heads) : 1;
     if (resident <= 0)
       return GKV_ERR_HIP;
     n_wg = std::max<int64_t>(resident, min_wg);
+    if (n_wg > kMaxWorkgroups)
+      return GKV_ERR_ARG;
   }
-  if (n_wg > kMaxWorkgroups)
-    return GKV_ERR_ARG;
   a.q = q;
   a.q_stride = q_stride;
   a.cos_tab = cos_tab;
@@ -672,16 +723,19 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
   a.num_blocks = cache.num_blocks;
   a.n_kv_heads = cache.n_kv_heads;
   a.window = window;
-  a.max_len = (int)n_max;
+  a.max_len = (int)(window > 0 ? std::min(max_seq_len, window) : max_seq_len);
   a.sinks = sinks;
   a.G = G;
   a.B = B;
   a.n_wg = (int)n_wg;
   a.fixed_S = split_tokens;
-  a.prio = prio_enabled();
-  a.plan = (int32_t *)workspace;
-  a.ws_o = (float *)((char *)workspace + plan_bytes(B));
-  a.ws_ml = a.ws_o + (size_t)(B + kMaxWorkgroups) * cache.n_kv_heads * kPartFloats;
+  char *ws = (char *)workspace;
+  a.plan = (int32_t *)(ws + L.plan);
+  a.flat = (int32_t *)(ws + L.flat);
+  a.steps = (int32_t *)(ws + L.steps);
+  a.qops = (u32x4 *)(ws + L.qops);
+  a.ws_o = (float *)(ws + L.ws_o);
+  a.ws_ml = (float *)(ws + L.ws_ml);
   a.out = out;
   a.out_stride = out_stride;
   a.out_bf16 = out_dtype == GKV_BF16;
@@ -689,20 +743,30 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
   return GKV_OK;
 }
 
-static int launch_split(const DecodeArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL(decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, a);
-  if (int st = launch_status("decode_plan_kernel"))
+static int launch_split(const DecodeArgs &a, int64_t t_max, hipStream_t s) {
+  const int waves = kPrepThreads / 64;
+  const int64_t by_items = (a.B * a.n_kv_heads + waves - 1) / waves;
+  const int64_t by_blocks = (t_max / kBlockTokens + kPrepThreads - 1) / kPrepThreads;
+  const int prep_wgs = (int)std::max<int64_t>(1, std::min<int64_t>(1024, std::max(by_items, by_blocks)));
+  hipLaunchKernelGGL(decode_prep_kernel, dim3(prep_wgs), dim3(kPrepThreads), 0, s, a);
+  if (int st = launch_status("decode_prep_kernel"))
     return st;
-  const dim3 grid(a.n_wg), block(64 * a.n_kv_heads);
+  const dim3 grid(a.n_wg), block(split_block(a.n_kv_heads));
   switch (ring_depth()) {
-  case 3:
-    hipLaunchKernelGGL(decode_split_kernel<3>, grid, block, 0, s, a);
+  case 4:
+    launch_split_ring<4>(a, grid, block, s);
     break;
-  case 2:
-    hipLaunchKernelGGL(decode_split_kernel<2>, grid, block, 0, s, a);
+  case 6:
+    launch_split_ring<6>(a, grid, block, s);
+    break;
+  case 7:
+    launch_split_ring<7>(a, grid, block, s);
+    break;
+  case 8:
+    launch_split_ring<8>(a, grid, block, s);
     break;
   default:
-    hipLaunchKernelGGL(decode_split_kernel<4>, grid, block, 0, s, a);
+    launch_split_ring<5>(a, grid, block, s);
   }
   return launch_status("decode_split_kernel");
 }
@@ -718,12 +782,10 @@ using namespace gkv;
 
 extern "C" size_t gkv_decode_workspace_bytes(int32_t B, int32_t n_kv_heads, int32_t max_seq_len,
                                              int32_t window, int32_t split_tokens) {
-  (void)max_seq_len;
-  (void)window;
   (void)split_tokens;
-  if (B < 0 || n_kv_heads <= 0)
+  if (B < 0 || n_kv_heads <= 0 || max_seq_len < 0 || window < 0)
     return 0;
-  return workspace_bytes(B, n_kv_heads);
+  return layout_of(B, n_kv_heads, stream_max(B, max_seq_len, window)).total;
 }
 
 extern "C" int gkv_decode_split(void *stream, int32_t B, int32_t n_q_heads, const float *q,
@@ -739,7 +801,7 @@ extern "C" int gkv_decode_split(void *stream, int32_t B, int32_t n_q_heads, cons
                          out_stride, out_dtype, dev_err, true);
   if (st != GKV_OK || B == 0)
     return st;
-  return launch_split(a, (hipStream_t)stream);
+  return launch_split(a, stream_max(B, max_seq_len, window), (hipStream_t)stream);
 }
 
 extern "C" int gkv_decode_combine(void *stream, int32_t B, int32_t n_q_heads, int32_t n_kv_heads,
@@ -771,7 +833,7 @@ extern "C" int gkv_decode_attention(void *stream, int32_t B, int32_t n_q_heads, 
                    out_dtype, dev_err, true);
   if (st != GKV_OK || B == 0)
     return st;
-  if ((st = launch_split(a, (hipStream_t)stream)))
+  if ((st = launch_split(a, stream_max(B, max_seq_len, window), (hipStream_t)stream)))
     return st;
   return launch_combine(a, (hipStream_t)stream);
 }
