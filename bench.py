@@ -83,9 +83,12 @@ def fill_cache(torch, gkv, pool, n_layers, dev, seed):
             del t
 
 
-def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, threads):
-    """Time the CPU oracle on a bounded sample of the workload (sequences
-    0..sample_seqs-1 of layer 0) and check the GPU output on it."""
+def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, threads,
+                 min_seconds):
+    """Time the CPU oracle on a bounded sample of the workload: the attention of
+    sequences 0..sample_seqs-1 of one layer over their cached K/V, repeated
+    until min_seconds of wall time have passed; also checks the GPU output of
+    those sequences against it (max-abs 2e-3 + rel 1e-2)."""
     sys.path.insert(0, ROOT)
     from oracle import kv_oracle as O
 
@@ -114,9 +117,15 @@ def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, th
     pos = seq_lens - 1
     q_rot, _, _, _ = O.kv_append(qkv, Hq, Hkv, cos, sin, pos)
     sinks = layer_state.sinks.cpu().numpy()
+    reps = 0
     t0 = time.perf_counter()
-    ref = O.decode_attention(q_rot, kc, vc, pos, sinks, window=W, ring=W, n_threads=threads)
-    dt = time.perf_counter() - t0
+    while True:
+        ref = O.decode_attention(q_rot, kc, vc, pos, sinks, window=W, ring=W, n_threads=threads)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds or reps >= 1000:
+            break
+    dt /= reps
     n_read = np.minimum(seq_lens, W) if W else seq_lens
     nbytes = float(n_read.sum()) * Hkv * D * 2 * 2
     got = gpu_out[:sample_seqs].float().cpu().numpy().reshape(sample_seqs, Hq, D)
@@ -124,8 +133,8 @@ def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, th
     ok = bool(np.all(err <= 2e-3 + 1e-2 * np.abs(ref)))
     return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=threads, kind="port",
                 sample=f"{sample_seqs} sequences of layer 0 ({int(n_read.sum())} cached tokens, "
-                       f"{nbytes / 1e6:.1f} MB of K+V), one decode attention, "
-                       f"{dt:.2f} s wall on {threads} OpenMP threads",
+                       f"{nbytes / 1e6:.1f} MB of K+V), one decode attention of one layer, "
+                       f"{reps} passes, {dt:.3f} s wall per pass on {threads} OpenMP threads",
                 seconds=round(dt, 3), gpu_matches=ok, max_abs_err=float(err.max()))
 
 
@@ -175,8 +184,10 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     ap.add_argument("--split-tokens", type=int, default=0)
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--cpu-sample", type=int, default=128,
-                    help="sequences timed on the CPU oracle (0: skip)")
+    ap.add_argument("--cpu-sample", type=int, default=-1,
+                    help="sequences timed on the CPU oracle (-1: the whole batch, 0: skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="repeat the CPU pass until this much wall time has passed")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--lengths", default="random", choices=["random", "sorted", "fixed"],
                     help="diagnostics: context lengths in batch order as drawn, sorted "
@@ -244,24 +255,20 @@ def main() -> int:
 
     def step(record: bool):
         for li, layer in enumerate(layers):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(5)] if record else None
             if record:
-                e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
                 e[0].record(stream)
             gkv.kv_append(layer.qkv, Hq, cos_d, sin_d, pos_d, layer.view, seq_lens=lens_d,
                           dev_err=err_d, stream=stream)
+            for i, stage in enumerate(("prepare", "split", "combine")):
+                if record:
+                    e[i + 1].record(stream)
+                gkv.decode_attention(layer.qkv, lens_d, max_len, layer.view, layer.sinks,
+                                     layer.out, window=layer.window, cos_tab=cos_d,
+                                     sin_tab=sin_d, split_tokens=args.split_tokens, workspace=ws,
+                                     dev_err=err_d, stream=stream, stage=stage)
             if record:
-                e[1].record(stream)
-            gkv.decode_attention(layer.qkv, lens_d, max_len, layer.view, layer.sinks, layer.out,
-                                 window=layer.window, cos_tab=cos_d, sin_tab=sin_d,
-                                 split_tokens=args.split_tokens, workspace=ws, dev_err=err_d,
-                                 stream=stream, stage="split")
-            if record:
-                e[2].record(stream)
-            gkv.decode_attention(layer.qkv, lens_d, max_len, layer.view, layer.sinks, layer.out,
-                                 window=layer.window, split_tokens=args.split_tokens,
-                                 workspace=ws, stream=stream, stage="combine")
-            if record:
-                e[3].record(stream)
+                e[4].record(stream)
                 ev.setdefault(li, []).append(e)
 
     for _ in range(args.warmup):
@@ -287,19 +294,13 @@ def main() -> int:
     for _ in range(args.steps):
         step(True)
     torch.cuda.synchronize()
-    split_ms = append_ms = combine_ms = 0.0
-    split_bytes = 0.0
+    stage_ms = np.zeros(4)  # append, prepare, split, combine (summed over layers)
     for li, lst in ev.items():
-        a = np.mean([e[0].elapsed_time(e[1]) for e in lst])
-        s = np.mean([e[1].elapsed_time(e[2]) for e in lst])
-        c = np.mean([e[2].elapsed_time(e[3]) for e in lst])
-        append_ms += a
-        split_ms += s
-        combine_ms += c
+        stage_ms += [np.mean([e[i].elapsed_time(e[i + 1]) for e in lst]) for i in range(4)]
     # dominant kernel: the split kernel of the full-attention layers (or of the
     # window layers when there are no full ones)
     full = [i for i, l in enumerate(layers) if not l.window] or list(range(len(layers)))
-    dom_ms = float(np.mean([np.mean([e[1].elapsed_time(e[2]) for e in ev[i]]) for i in full]))
+    dom_ms = float(np.mean([np.mean([e[2].elapsed_time(e[3]) for e in ev[i]]) for i in full]))
     dom_bytes = float(np.mean([bytes_of(layers[i]) for i in full]))
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
 
@@ -310,10 +311,11 @@ def main() -> int:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
     cpu = None
-    if args.cpu_sample > 0:
+    if args.cpu_sample != 0:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        n_cpu = B if args.cpu_sample < 0 else min(args.cpu_sample, B)
         cpu = cpu_baseline(torch, gkv, pool, layers[full[0]], L, cfg, layers[full[0]].out,
-                           min(args.cpu_sample, B), threads)
+                           n_cpu, threads, args.cpu_seconds)
 
     value = kv_bytes / (ms_per_step * 1e-3) / 1e9
     line = {
@@ -335,8 +337,8 @@ def main() -> int:
             "context": f"U[{cfg['lo']},{cfg['hi']}]", "window": cfg["window"],
             "kv_bytes_per_step": kv_bytes, "split_tokens": args.split_tokens or 512,
             "pool_bytes": pool.device_bytes(),
-            "kernel_ms": {"append": round(append_ms, 4), "split": round(split_ms, 4),
-                          "combine": round(combine_ms, 4)},
+            "kernel_ms": dict(zip(("append", "prepare", "split", "combine"),
+                                  (round(float(x), 4) for x in stage_ms))),
             "parallelism": "1 GPU",
         },
         "roofline": {

@@ -14,7 +14,7 @@
  *                            (and rope_exact + kv_write_kernel, kernels/misc.hpp:55-85)
  *   gkv_decode_attention  <- attention_q8v_chunk64 / attention_bf16_chunk64 / attention_bf16,
  *                            getp-csrc/kernels/fast_attention.hpp:604-622, 566-580, 525-547
- *   gkv_decode_split, gkv_decode_combine
+ *   gkv_decode_prepare, gkv_decode_split, gkv_decode_combine
  *                         <- the per-wave split and the LDS merge inside
  *                            attention_gqa8_kernel, fast_attention.hpp:164-425 (a7: 383-424)
  *   gkv_prefill_attention <- no reference kernel; the reference feeds prompts one
@@ -133,8 +133,7 @@ size_t gkv_decode_workspace_bytes(int32_t B, int32_t n_kv_heads, int32_t max_seq
  *             (a multiple of 32, at most 4096)
  *   max_seq_len   host upper bound of seq_lens (sizes the grid)
  *   out       [B][out_stride] of out_dtype, heads at h*64
- * Launches gkv_decode_split then, when some sequence has more than one split,
- * gkv_decode_combine. */
+ * Launches gkv_decode_prepare, gkv_decode_split and gkv_decode_combine. */
 int gkv_decode_attention(void *stream, int32_t B, int32_t n_q_heads, const float *q,
                          int64_t q_stride, const float *cos_tab, const float *sin_tab,
                          const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,
@@ -142,10 +141,20 @@ int gkv_decode_attention(void *stream, int32_t B, int32_t n_q_heads, const float
                          void *workspace, size_t workspace_bytes, void *out, int64_t out_stride,
                          int32_t out_dtype, uint32_t *dev_err);
 
-/* The two stages of gkv_decode_attention, for callers that time or schedule
- * them separately. Same arguments. gkv_decode_split writes the final output of
- * every sequence that fits in one split, and per-split partial results of the
- * others into the workspace; gkv_decode_combine merges those with the sink. */
+/* The three launches of gkv_decode_attention, for callers that time or
+ * schedule them separately; same arguments, run in this order on one stream
+ * with the same workspace. gkv_decode_prepare lays the sequences out as one
+ * token stream cut into equal ranges (block ids checked against the pool,
+ * per-step records) and prepares the rotated, scaled query operands;
+ * gkv_decode_split streams every range, writes the final output of each
+ * sequence that lies in one range and partial results of the others into the
+ * workspace; gkv_decode_combine merges those with the sink. */
+int gkv_decode_prepare(void *stream, int32_t B, int32_t n_q_heads, const float *q,
+                       int64_t q_stride, const float *cos_tab, const float *sin_tab,
+                       const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,
+                       int32_t window, const float *sinks, int32_t split_tokens, void *workspace,
+                       size_t workspace_bytes, void *out, int64_t out_stride, int32_t out_dtype,
+                       uint32_t *dev_err);
 int gkv_decode_split(void *stream, int32_t B, int32_t n_q_heads, const float *q,
                      int64_t q_stride, const float *cos_tab, const float *sin_tab,
                      const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,

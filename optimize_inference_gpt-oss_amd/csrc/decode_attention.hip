@@ -743,14 +743,17 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
   return GKV_OK;
 }
 
-static int launch_split(const DecodeArgs &a, int64_t t_max, hipStream_t s) {
+static int launch_prep(const DecodeArgs &a, int64_t t_max, hipStream_t s) {
   const int waves = kPrepThreads / 64;
   const int64_t by_items = (a.B * a.n_kv_heads + waves - 1) / waves;
   const int64_t by_blocks = (t_max / kBlockTokens + kPrepThreads - 1) / kPrepThreads;
-  const int prep_wgs = (int)std::max<int64_t>(1, std::min<int64_t>(1024, std::max(by_items, by_blocks)));
+  const int prep_wgs =
+      (int)std::max<int64_t>(1, std::min<int64_t>(1024, std::max(by_items, by_blocks)));
   hipLaunchKernelGGL(decode_prep_kernel, dim3(prep_wgs), dim3(kPrepThreads), 0, s, a);
-  if (int st = launch_status("decode_prep_kernel"))
-    return st;
+  return launch_status("decode_prep_kernel");
+}
+
+static int launch_split(const DecodeArgs &a, hipStream_t s) {
   const dim3 grid(a.n_wg), block(split_block(a.n_kv_heads));
   switch (ring_depth()) {
   case 4:
@@ -788,20 +791,31 @@ extern "C" size_t gkv_decode_workspace_bytes(int32_t B, int32_t n_kv_heads, int3
   return layout_of(B, n_kv_heads, stream_max(B, max_seq_len, window)).total;
 }
 
-extern "C" int gkv_decode_split(void *stream, int32_t B, int32_t n_q_heads, const float *q,
-                                int64_t q_stride, const float *cos_tab, const float *sin_tab,
-                                const int32_t *seq_lens, int32_t max_seq_len,
-                                gkv_cache_view cache, int32_t window, const float *sinks,
-                                int32_t split_tokens, void *workspace, size_t workspace_bytes_,
-                                void *out, int64_t out_stride, int32_t out_dtype,
-                                uint32_t *dev_err) {
+#define GKV_DECODE_PARAMS                                                                   \
+  void *stream, int32_t B, int32_t n_q_heads, const float *q, int64_t q_stride,                \
+      const float *cos_tab, const float *sin_tab, const int32_t *seq_lens, int32_t max_seq_len, \
+      gkv_cache_view cache, int32_t window, const float *sinks, int32_t split_tokens,          \
+      void *workspace, size_t workspace_bytes_, void *out, int64_t out_stride,                  \
+      int32_t out_dtype, uint32_t *dev_err
+#define GKV_DECODE_PREPARE(a)                                                                  \
+  prepare(a, B, n_q_heads, q, q_stride, cos_tab, sin_tab, seq_lens, max_seq_len, cache, window, \
+          sinks, split_tokens, workspace, workspace_bytes_, out, out_stride, out_dtype, dev_err, \
+          true)
+
+extern "C" int gkv_decode_prepare(GKV_DECODE_PARAMS) {
   DecodeArgs a;
-  const int st = prepare(a, B, n_q_heads, q, q_stride, cos_tab, sin_tab, seq_lens, max_seq_len,
-                         cache, window, sinks, split_tokens, workspace, workspace_bytes_, out,
-                         out_stride, out_dtype, dev_err, true);
+  const int st = GKV_DECODE_PREPARE(a);
   if (st != GKV_OK || B == 0)
     return st;
-  return launch_split(a, stream_max(B, max_seq_len, window), (hipStream_t)stream);
+  return launch_prep(a, stream_max(B, max_seq_len, window), (hipStream_t)stream);
+}
+
+extern "C" int gkv_decode_split(GKV_DECODE_PARAMS) {
+  DecodeArgs a;
+  const int st = GKV_DECODE_PREPARE(a);
+  if (st != GKV_OK || B == 0)
+    return st;
+  return launch_split(a, (hipStream_t)stream);
 }
 
 extern "C" int gkv_decode_combine(void *stream, int32_t B, int32_t n_q_heads, int32_t n_kv_heads,
@@ -820,20 +834,14 @@ extern "C" int gkv_decode_combine(void *stream, int32_t B, int32_t n_q_heads, in
   return launch_combine(a, (hipStream_t)stream);
 }
 
-extern "C" int gkv_decode_attention(void *stream, int32_t B, int32_t n_q_heads, const float *q,
-                                    int64_t q_stride, const float *cos_tab, const float *sin_tab,
-                                    const int32_t *seq_lens, int32_t max_seq_len,
-                                    gkv_cache_view cache, int32_t window, const float *sinks,
-                                    int32_t split_tokens, void *workspace,
-                                    size_t workspace_bytes_, void *out, int64_t out_stride,
-                                    int32_t out_dtype, uint32_t *dev_err) {
+extern "C" int gkv_decode_attention(GKV_DECODE_PARAMS) {
   DecodeArgs a;
-  int st = prepare(a, B, n_q_heads, q, q_stride, cos_tab, sin_tab, seq_lens, max_seq_len, cache,
-                   window, sinks, split_tokens, workspace, workspace_bytes_, out, out_stride,
-                   out_dtype, dev_err, true);
+  int st = GKV_DECODE_PREPARE(a);
   if (st != GKV_OK || B == 0)
     return st;
-  if ((st = launch_split(a, stream_max(B, max_seq_len, window), (hipStream_t)stream)))
+  if ((st = launch_prep(a, stream_max(B, max_seq_len, window), (hipStream_t)stream)))
+    return st;
+  if ((st = launch_split(a, (hipStream_t)stream)))
     return st;
   return launch_combine(a, (hipStream_t)stream);
 }

@@ -64,6 +64,9 @@ SIGNATURES = {
     "gkv_decode_attention": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
                                             CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64,
                                             _i32, _vp]),
+    "gkv_decode_prepare": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
+                                        CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
+                                        _vp]),
     "gkv_decode_split": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
                                         CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
                                         _vp]),
@@ -202,12 +205,13 @@ def decode_attention(q, seq_lens, max_seq_len, view: CacheView, sinks, out, wind
     out_dtype = BF16 if out.dtype == torch.bfloat16 else F32
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     args_common = (stream_handle(stream), q.shape[0])
-    if stage in ("both", "split"):
-        fn = lib().gkv_decode_attention if stage == "both" else lib().gkv_decode_split
-        st = fn(*args_common, sinks.shape[0], ptr(q), q.stride(0), ptr(cos_tab), ptr(sin_tab),
+    if stage in ("both", "prepare", "split"):
+        name = {"both": "gkv_decode_attention", "prepare": "gkv_decode_prepare",
+                "split": "gkv_decode_split"}[stage]
+        st = getattr(lib(), name)(*args_common, sinks.shape[0], ptr(q), q.stride(0), ptr(cos_tab), ptr(sin_tab),
                 ptr(seq_lens), max_seq_len, view, window, ptr(sinks), split_tokens,
                 ptr(workspace), ws_bytes, ptr(out), out.stride(0), out_dtype, ptr(dev_err))
-        check("gkv_decode_attention" if stage == "both" else "gkv_decode_split", st)
+        check(name, st)
     if stage == "combine":
         st = lib().gkv_decode_combine(*args_common, sinks.shape[0], view.n_kv_heads,
                                       ptr(seq_lens), max_seq_len, window, ptr(sinks),
