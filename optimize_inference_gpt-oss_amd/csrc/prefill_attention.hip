@@ -1,7 +1,322 @@
-// placeholder
+// Causal attention of a packed batch of prompts with per-head sinks and the
+// sliding window, on bf16 matrix cores.
+//
+// The reference has no prefill kernel: it feeds a prompt one token at a time
+// through the decode step (getp-csrc/engine/gpu_engine.hpp:811-813), so each
+// query row j of a prompt is the decode attention of run.cpp:597-642 at
+// pos = j -- over that prompt's positions 0..j (window W: j-W+1..j) plus the
+// sink logit. This kernel computes exactly that for all rows at once.
+//
+// Work: one workgroup per (prompt, kv head, block of 32 query positions), one
+// wave per query head of the kv head's group (all waves share the K/V tiles
+// in LDS, so each K/V byte is read from L2 once per group). Blocks are
+// launched longest-first (the last query blocks of the prompts see the most
+// keys).
+//
+// Matrix cores, v_mfma_f32_16x16x32_bf16 (the decode kernel's operand
+// arrangement, with 16 query columns instead of 8 heads):
+//   scores  S^T[key][query] = K[key][dims] * Q^T[dims][query]; the query is
+//           carried as bf16 high + low pieces accumulated into one tile, so
+//           the scores keep ~16 mantissa bits of the fp32 query
+//   output  O^T[dim][query] += V^T[dim][keys] * P^T[keys][query], P again as
+//           bf16 high + low pieces (a single bf16 P leaves errors of 2^-9 of
+//           |v| on queries that see few keys)
+//   A 32-key step uses two 16-key score tiles; lane (kg, n) holds keys
+//   4kg..4kg+3 of each, which are its P^T operand slots; the V^T operand is
+//   the same 8 keys of one dim, read from V stored transposed in LDS.
+// Online softmax in the log2 domain (scale 1/8 * log2 e folded into Q), lazy
+// rescale by threshold 8, the running max seeded with the sink, and the sink
+// added in the final normalisation, as in the decode kernel.
+//
+// LDS: K tile [64 keys][64 dims + 8 pad], V^T tile [64 dims][64 keys + 8 pad],
+// double-buffered (36 KB); tile t + 1 is fetched into registers while tile t
+// is consumed.
 #include "gkv_device.hpp"
-extern "C" int gkv_prefill_attention(void *, int32_t, const int32_t *, int32_t, int32_t, int32_t,
-                                     const float *, int64_t, const void *, const void *,
-                                     const float *, int32_t, void *, int64_t, int32_t) {
-  return GKV_ERR_UNSUPPORTED;
+
+namespace gkv {
+
+constexpr int kQBlock = 32;         // query positions per workgroup
+constexpr int kKTile = 64;          // keys per LDS tile
+constexpr int kKRow = kHeadDim + 8; // bf16 per K row in LDS (pad against bank conflicts)
+constexpr int kVRow = kKTile + 8;   // bf16 per V^T row in LDS
+
+struct PrefillArgs {
+  const int32_t *cu;
+  const float *q;
+  int64_t q_stride;
+  const uint16_t *k, *v;
+  int64_t kv_stride; // elements per packed row: Hkv * 64
+  const float *sinks;
+  int B, G, n_kv_heads, window, n_qblocks;
+  void *out;
+  int64_t out_stride;
+  int out_bf16;
+};
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void prefill_kernel(PrefillArgs a) {
+  constexpr int D = kHeadDim;
+  constexpr int NT = NW * 64;
+  constexpr int kLoads = kKTile * (D / 8) / NT; // 16-byte pieces of K (and of V) per thread per tile
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kKTile * kKRow];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][D * kVRow];
+
+  int id = blockIdx.x;
+  const int g = id % a.n_kv_heads;
+  id /= a.n_kv_heads;
+  const int b = id % a.B;
+  const int qb = a.n_qblocks - 1 - id / a.B; // longest work first
+  const int row0 = a.cu[b];
+  const int L = a.cu[b + 1] - row0;
+  const int q0 = qb * kQBlock;
+  if (q0 >= L)
+    return;
+  const int q_last = min(q0 + kQBlock, L) - 1;
+  const int W = a.window;
+  int k_lo = W > 0 ? max(0, q0 - W + 1) : 0;
+  k_lo &= ~(kKTile - 1);
+  const int n_tiles = (q_last + 1 - k_lo + kKTile - 1) / kKTile;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = uniform(tid >> 6);
+  const int n = lane & 15, kg = lane >> 4;
+  const bool active = wave < a.G;
+  const int h = g * a.G + (active ? wave : 0);
+
+  // ---- K/V tile staging: thread piece i covers key (tid + i*NT) / 8, dims 8 * ((tid + i*NT) % 8)
+  u32x4 kreg[kLoads], vreg[kLoads];
+  auto fetch = [&](int t) {
+    const int kt0 = k_lo + t * kKTile;
+#pragma unroll
+    for (int i = 0; i < kLoads; i++) {
+      const int idx = tid + i * NT;
+      const int key = idx >> 3, part = idx & 7;
+      const int row = row0 + min(kt0 + key, L - 1); // clamped: rows past the prompt are masked
+      const int64_t off = (int64_t)row * a.kv_stride + g * D + part * 8;
+      kreg[i] = *(const u32x4 *)(a.k + off);
+      vreg[i] = *(const u32x4 *)(a.v + off);
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kLoads; i++) {
+      const int idx = tid + i * NT;
+      const int key = idx >> 3, part = idx & 7;
+      *(u32x4 *)&k_lds[buf][key * kKRow + part * 8] = kreg[i];
+      const uint16_t *vv = (const uint16_t *)&vreg[i];
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        v_lds[buf][(part * 8 + j) * kVRow + key] = vv[j];
+    }
+  };
+
+  // ---- query operands: column tile c holds queries q0 + 16c + n; half dh dims 32dh + 8kg + j
+  bf16x8 qhi[2][2], qlo[2][2];
+  {
+    const float qscale = 0.125f * kLog2e; // 1/sqrt(64); exp -> exp2
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      const int row = row0 + min(q0 + 16 * c + n, L - 1);
+      const float *qp = a.q + (int64_t)row * a.q_stride + h * D + 8 * kg;
+#pragma unroll
+      for (int dh = 0; dh < 2; dh++) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const float x = qp[32 * dh + j] * qscale;
+          const __bf16 hi = (__bf16)x;
+          qhi[c][dh][j] = hi;
+          qlo[c][dh][j] = (__bf16)(x - (float)hi);
+        }
+      }
+    }
+  }
+  const float sink2 = a.sinks[h] * kLog2e;
+  float m_run[2] = {sink2, sink2}, lsum[2] = {0.0f, 0.0f};
+  f32x4 o[2][4];
+#pragma unroll
+  for (int c = 0; c < 2; c++)
+#pragma unroll
+    for (int nn = 0; nn < 4; nn++)
+      o[c][nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int t = 0; t < n_tiles; t++) {
+    const int buf = t & 1;
+    if (t + 1 < n_tiles)
+      fetch(t + 1);
+    const int kt0 = k_lo + t * kKTile;
+#pragma unroll
+    for (int s = 0; s < kKTile / 32; s++) {
+      const int kb = kt0 + 32 * s; // first key of the step
+      // uniform skips: every key after the last query, or (window) older
+      // than the first query's window
+      if (!active || kb > q_last || (W > 0 && kb + 31 <= q0 - W))
+        continue;
+      const bool need_mask = kb + 31 > q0 || (W > 0 && kb <= q_last - W);
+      f32x4 acc[2][2]; // [key tile][query column tile]
+#pragma unroll
+      for (int kt = 0; kt < 2; kt++) {
+        acc[kt][0] = acc[kt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int dh = 0; dh < 2; dh++) {
+          const bf16x8 kop =
+              *(const bf16x8 *)&k_lds[buf][(32 * s + 16 * kt + n) * kKRow + 32 * dh + 8 * kg];
+#pragma unroll
+          for (int c = 0; c < 2; c++) {
+            acc[kt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[c][dh], acc[kt][c], 0, 0, 0);
+            acc[kt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo[c][dh], acc[kt][c], 0, 0, 0);
+          }
+        }
+      }
+      bf16x8 phi[2], plo[2];
+#pragma unroll
+      for (int c = 0; c < 2; c++) {
+        float sc[8];
+#pragma unroll
+        for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            sc[4 * kt + r] = acc[kt][c][r];
+        if (need_mask) {
+          const int qa = q0 + 16 * c + n;
+#pragma unroll
+          for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              const int ka = kb + 16 * kt + 4 * kg + r;
+              if (ka > qa || (W > 0 && ka <= qa - W))
+                sc[4 * kt + r] = -INFINITY;
+            }
+        }
+        float mx = sc[0];
+#pragma unroll
+        for (int i = 1; i < 8; i++)
+          mx = fmaxf(mx, sc[i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // lazy rescale: the reference max moves only when exceeded by more than 8
+        if (__any(mx > m_run[c] + 8.0f)) {
+          const float m_new = fmaxf(m_run[c], mx);
+          const float alpha = __builtin_amdgcn_exp2f(m_run[c] - m_new);
+          m_run[c] = m_new;
+          lsum[c] *= alpha;
+#pragma unroll
+          for (int nn = 0; nn < 4; nn++)
+            o[c][nn] *= alpha;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const float p = __builtin_amdgcn_exp2f(sc[i] - m_run[c]);
+          lsum[c] += p;
+          const __bf16 hi = (__bf16)p;
+          phi[c][i] = hi;
+          plo[c][i] = (__bf16)(p - (float)hi);
+        }
+      }
+#pragma unroll
+      for (int nn = 0; nn < 4; nn++) {
+        const uint16_t *vrow = &v_lds[buf][(16 * nn + n) * kVRow + 32 * s + 4 * kg];
+        const u32x2 x = *(const u32x2 *)vrow;
+        const u32x2 y = *(const u32x2 *)(vrow + 16);
+        const bf16x8 vop = __builtin_bit_cast(bf16x8, u32x4{x[0], x[1], y[0], y[1]});
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+          o[c][nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, phi[c], o[c][nn], 0, 0, 0);
+          o[c][nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, plo[c], o[c][nn], 0, 0, 0);
+        }
+      }
+    }
+    if (t + 1 < n_tiles)
+      stash(buf ^ 1);
+    __syncthreads();
+  }
+  if (!active)
+    return;
+
+  // out = o * 2^(m - M) / (l * 2^(m - M) + 2^(sink - M)), M = max(m, sink)
+#pragma unroll
+  for (int c = 0; c < 2; c++) {
+    float ls = lsum[c];
+    ls += __shfl_xor(ls, 16);
+    ls += __shfl_xor(ls, 32);
+    const int qa = q0 + 16 * c + n;
+    if (qa >= L)
+      continue;
+    const float M2 = fmaxf(m_run[c], sink2);
+    const float f = __builtin_amdgcn_exp2f(m_run[c] - M2);
+    const float scale = f / fmaf(ls, f, __builtin_amdgcn_exp2f(sink2 - M2));
+    const int64_t ob = (int64_t)(row0 + qa) * a.out_stride + (int64_t)h * D + 4 * kg;
+#pragma unroll
+    for (int nn = 0; nn < 4; nn++) {
+      const f32x4 r = o[c][nn] * scale;
+      if (a.out_bf16) {
+        typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+        *(bf16x4 *)((__bf16 *)a.out + ob + 16 * nn) =
+            bf16x4{(__bf16)r[0], (__bf16)r[1], (__bf16)r[2], (__bf16)r[3]};
+      } else {
+        *(f32x4 *)((float *)a.out + ob + 16 * nn) = r;
+      }
+    }
+  }
+}
+
+} // namespace gkv
+
+extern "C" int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_seqlens,
+                                     int32_t max_len, int32_t n_q_heads, int32_t n_kv_heads,
+                                     const float *q, int64_t q_stride, const void *k,
+                                     const void *v, const float *sinks, int32_t window, void *out,
+                                     int64_t out_stride, int32_t out_dtype) {
+  using namespace gkv;
+  if (B < 0 || max_len < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || window < 0 ||
+      (out_dtype != GKV_F32 && out_dtype != GKV_BF16))
+    return GKV_ERR_ARG;
+  if (B > 0 && (!cu_seqlens || !q || !k || !v || !sinks || !out))
+    return GKV_ERR_ARG;
+  if (n_q_heads % n_kv_heads != 0)
+    return GKV_ERR_ARG;
+  const int G = n_q_heads / n_kv_heads;
+  if (G > 8)
+    return GKV_ERR_UNSUPPORTED;
+  if (q_stride < (int64_t)n_q_heads * kHeadDim || out_stride < (int64_t)n_q_heads * kHeadDim ||
+      (q_stride % 4) != 0)
+    return GKV_ERR_ARG;
+  if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)q) % 16 != 0)
+    return GKV_ERR_ARG; // 16-byte vector loads
+  const int n_qblocks = (max_len + kQBlock - 1) / kQBlock;
+  const int64_t grid = (int64_t)n_qblocks * B * n_kv_heads;
+  if (grid == 0)
+    return GKV_OK;
+  if (grid >= INT32_MAX)
+    return GKV_ERR_ARG;
+  PrefillArgs a;
+  a.cu = cu_seqlens;
+  a.q = q;
+  a.q_stride = q_stride;
+  a.k = (const uint16_t *)k;
+  a.v = (const uint16_t *)v;
+  a.kv_stride = (int64_t)n_kv_heads * kHeadDim;
+  a.sinks = sinks;
+  a.B = B;
+  a.G = G;
+  a.n_kv_heads = n_kv_heads;
+  a.window = window;
+  a.n_qblocks = n_qblocks;
+  a.out = out;
+  a.out_stride = out_stride;
+  a.out_bf16 = out_dtype == GKV_BF16;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 g((unsigned)grid);
+  if (G > 4)
+    hipLaunchKernelGGL(prefill_kernel<8>, g, dim3(512), 0, s, a);
+  else if (G > 2)
+    hipLaunchKernelGGL(prefill_kernel<4>, g, dim3(256), 0, s, a);
+  else if (G > 1)
+    hipLaunchKernelGGL(prefill_kernel<2>, g, dim3(128), 0, s, a);
+  else
+    hipLaunchKernelGGL(prefill_kernel<1>, g, dim3(64), 0, s, a);
+  return launch_status("prefill_kernel");
 }
