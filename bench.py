@@ -10,7 +10,11 @@ workload: BASELINE config 2, the gpt-oss-20b-shape full-attention decode layer
 randomly permuted block table, context lengths U[128, 2048], values
 N(0,1)*0.5, sinks N(0,1)). Config 3 is the 128-token sliding-window layer
 (ring of 128 slots, lengths U[1, 4096]); config 5 the 36-layer gpt-oss-120b
-step (B=1024, alternating window/full layers, lengths U[1024, 3072]).
+step (B=1024, alternating window/full layers, lengths U[1024, 3072]). Config 4
+is the prefill path: every token of 64 prompts (lengths U[64, 512]) appended
+into an empty paged pool, then causal attention with sinks, for one
+128-window and one full layer; its line reports TFLOP/s against the bf16
+matrix-core peak.
 
 Inputs are synthetic and resident in HBM before the timed region. The JSON
 line's value is algorithmic KV-read bytes per step / step time (GB/s); the
@@ -45,11 +49,15 @@ def load_gkv():
     return mod
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
 CONFIGS = {
     2: dict(name="gpt-oss-20b full-attention decode layer", B=512, Hq=64, Hkv=8, lo=128,
             hi=2048, layers=1, window=0),
     3: dict(name="gpt-oss sliding-window decode layer", B=512, Hq=64, Hkv=8, lo=0, hi=4095,
             layers=1, window=128),
+    4: dict(name="batched causal prefill chunk (full + 128-window layer)", B=64, Hq=64, Hkv=8,
+            lo=64, hi=512, layers=2, window=128),
     5: dict(name="gpt-oss-120b 36-layer decode step", B=1024, Hq=64, Hkv=8, lo=1024, hi=3072,
             layers=36, window=128),
 }
@@ -176,6 +184,125 @@ def copy_calibration(torch, args) -> int:
     return 0
 
 
+def run_prefill(torch, gkv, args) -> int:
+    """Config 4: append every token of B prompts into an empty paged pool, then
+    causal prefill attention, for one 128-window layer and one full layer."""
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[4]
+    B, Hq, Hkv = cfg["B"], cfg["Hq"], cfg["Hkv"]
+    rng = np.random.default_rng(args.seed)
+    L = rng.integers(cfg["lo"], cfg["hi"] + 1, size=B).astype(np.int32)
+    T = int(L.sum())
+    max_len = int(L.max())
+    cu = np.concatenate([[0], np.cumsum(L)]).astype(np.int32)
+    pos = np.concatenate([np.arange(l) for l in L]).astype(np.int32)
+    row_seq = np.repeat(np.arange(B), L).astype(np.int32)
+    need = int(((L + 15) // 16).sum())
+    pool = gkv.Pool(n_layers=2, n_kv_heads=Hkv, max_seqs=B, max_seq_len=max_len,
+                    window=cfg["window"], num_blocks=need + 64, shuffle_seed=args.seed)
+    for b in range(B):
+        assert pool.seq_alloc() == b
+        if pool.reserve(b, int(L[b])) != 0:
+            raise RuntimeError("pool reserve failed")
+    pool.sync()
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    cos, sin = gkv.rope_table(max_len)
+    cos_d, sin_d, cu_d, pos_d, seq_d, lens_d = map(t, (cos, sin, cu, pos, row_seq, L))
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    layers = []
+    for li in range(2):
+        g = torch.Generator(device=dev)
+        g.manual_seed(args.seed * 100 + li)
+        view = pool.view(li)
+        layers.append(dict(
+            view=view, window=view.ring,
+            qkv=torch.randn(T, (Hq + 2 * Hkv) * D, generator=g, device=dev) * 0.5,
+            sinks=torch.randn(Hq, generator=g, device=dev),
+            q=torch.empty(T, Hq * D, device=dev),
+            k=torch.empty(T, Hkv * D, dtype=torch.bfloat16, device=dev),
+            v=torch.empty(T, Hkv * D, dtype=torch.bfloat16, device=dev),
+            out=torch.empty(T, Hq * D, dtype=torch.bfloat16, device=dev)))
+    stream = torch.cuda.current_stream()
+
+    def flops(window):
+        n = np.arange(1, max_len + 1)
+        if window:
+            n = np.minimum(n, window)
+        cum = np.concatenate([[0], np.cumsum(n)])
+        return 4.0 * Hq * D * float(cum[L].sum())
+
+    ev = []
+
+    def step(record):
+        for li, ly in enumerate(layers):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(3)] if record else None
+            if record:
+                e[0].record(stream)
+            gkv.kv_append(ly["qkv"], Hq, cos_d, sin_d, pos_d, ly["view"], row_seq=seq_d,
+                          seq_lens=lens_d, q_out=ly["q"], k_pack=ly["k"], v_pack=ly["v"],
+                          dev_err=err, stream=stream)
+            if record:
+                e[1].record(stream)
+            gkv.prefill_attention(cu_d, max_len, ly["q"], ly["k"], ly["v"], ly["sinks"],
+                                  ly["out"], Hkv, window=ly["window"], stream=stream)
+            if record:
+                e[2].record(stream)
+                ev.append((li, e))
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    if int(err.item()) != 0:
+        raise RuntimeError(f"device error word {int(err.item())}")
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(args.steps):
+        step(False)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+    for _ in range(args.steps):
+        step(True)
+    torch.cuda.synchronize()
+    kern = {}
+    for li, e in ev:
+        kern.setdefault(li, []).append((e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])))
+    fl = [flops(ly["window"]) for ly in layers]
+    full = [i for i, ly in enumerate(layers) if not ly["window"]][0]
+    dom_ms = float(np.mean([x[1] for x in kern[full]]))
+    achieved = fl[full] / (dom_ms * 1e-3) / 1e12
+    line = {
+        "metric": "causal prefill attention throughput (TFLOP/s), config 4",
+        "value": round(sum(fl) / (ms_per_step * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*0.5 q/k/v rows, N(0,1) sinks, permuted block table)",
+        "config": {
+            "workload": f"config 4: {cfg['name']}", "B": B, "H_q": Hq, "H_kv": Hkv,
+            "head_dim": D, "prompt_tokens": T, "lengths": f"U[{cfg['lo']},{cfg['hi']}]",
+            "kernel_ms": {("window" if layers[i]["window"] else "full"): {
+                "append": round(float(np.mean([x[0] for x in kern[i]])), 4),
+                "prefill": round(float(np.mean([x[1] for x in kern[i]])), 4)}
+                for i in kern},
+            "algorithmic_flops": {("window" if layers[i]["window"] else "full"): fl[i]
+                                  for i in range(len(layers))},
+            "parallelism": "1 GPU",
+        },
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "prefill_kernel", "kernel_us": round(dom_ms * 1e3, 2),
+                     "algorithmic_flops": fl[full]},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    pool.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -208,6 +335,8 @@ def main() -> int:
     if args.copy_mib:
         return copy_calibration(torch, args)
     gkv = load_gkv()
+    if args.config == 4:
+        return run_prefill(torch, gkv, args)
     dev = torch.device("cuda:0")
     cfg = CONFIGS[args.config]
     B, Hq, Hkv, n_layers = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["layers"]
