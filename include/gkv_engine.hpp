@@ -1,0 +1,97 @@
+// C++ engine shim: the attention entry points that the reference engine's
+// layer_attention calls (getp-csrc/engine/gpu_engine.hpp:495-498), kept
+// under their names and argument order and forwarded to the gkv C ABI over
+// the paged cache.
+//
+// What changes for the caller is the cache description: the reference passes
+// one contiguous cache per layer (kc16 / vq8 / vs, slots) and one position
+// for the whole batch; here a layer is a gkv_cache_view into the paged pool
+// and every row carries its own position (continuous batching). Error
+// behaviour is the reference's: a failed call prints and exits, like its
+// HIP_CHECK (gpu_engine.hpp:41-49); callers who want the status use the C ABI
+// directly.
+#ifndef GKV_ENGINE_HPP
+#define GKV_ENGINE_HPP
+
+#include <cstdio>
+#include <cstdlib>
+
+#include "gkv.h"
+
+namespace gkv_engine {
+
+typedef uint16_t bf16_t; // raw bfloat16 bits (as getp-csrc/kernels/fast_common.hpp:7)
+typedef void *stream_t;  // a hipStream_t
+
+// Per-step state of the batch. The reference keeps a scalar pos for the
+// whole batch and device pointers to row pos of the cos/sin table
+// (gpu_engine.hpp:476); here each row has its own position.
+struct PagedBatch {
+  const int32_t *row_pos;  // device int32 [B]: position of each row's new token
+  const int32_t *seq_lens; // device int32 [B]: row_pos + 1
+  int32_t max_seq_len;     // host bound of seq_lens
+  const float *cos_tab;    // device gkv_rope_table rows [max_pos][32]
+  const float *sin_tab;
+  void *workspace;         // device, gkv_decode_workspace_bytes(B, Hkv, max_seq_len, 0, 0)
+  size_t workspace_bytes;
+  uint32_t *dev_err;       // device uint32 (GKV_DEVERR_* bits), or nullptr
+};
+
+// One layer's cache (replaces GpuLayer::kc16 / vq8 / vs / slots / window /
+// sinks, gpu_engine.hpp:59-78).
+struct PagedLayer {
+  gkv_cache_view view; // gkv_pool_layer_view(pool, l, &view)
+  int32_t window;      // 0 (full layer) or the ring size
+  const float *sinks;  // device fp32 [n_q_heads]
+};
+
+inline void check(int status, const char *what) {
+  if (status != GKV_OK) {
+    fprintf(stderr, "%s failed: %s%s%s\n", what, gkv_status_string(status),
+            status == GKV_ERR_HIP ? ": " : "", status == GKV_ERR_HIP ? gkv_last_error() : "");
+    exit(EXIT_FAILURE);
+  }
+}
+
+// rope_kv_bf16 (getp-csrc/kernels/fast_misc.hpp:112-127): RoPE on the K heads
+// (and, with rotate_q, the Q heads in place) of B qkv rows, and the bf16 store
+// of K and V at each row's position in the layer's paged cache.
+inline void rope_kv_bf16(stream_t s, int B, float *qkv, int row_stride, const PagedBatch &bt,
+                         int n_q_heads, const PagedLayer &layer, bool rotate_q = true) {
+  check(gkv_kv_append(s, B, qkv, row_stride, n_q_heads, bt.cos_tab, bt.sin_tab, bt.row_pos,
+                      nullptr, bt.seq_lens, layer.view, rotate_q ? qkv : nullptr, row_stride,
+                      nullptr, nullptr, bt.dev_err),
+        "rope_kv_bf16");
+}
+
+// attention_bf16_chunk64 (getp-csrc/kernels/fast_attention.hpp:566-580): one
+// query row per sequence against its cache plus the head's sink, output bf16
+// [B][out_stride]. With q_rotated false the query is rotated on load at
+// row_pos (the reference's cosv/sinv form, used after
+// rope_kv_bf16(rotate_q = false)).
+inline void attention_bf16_chunk64(stream_t s, const float *qkv, int row_stride,
+                                   const PagedLayer &layer, int n_q_heads, bf16_t *out,
+                                   int out_stride, int B, const PagedBatch &bt,
+                                   bool q_rotated = false) {
+  check(gkv_decode_attention(s, B, n_q_heads, qkv, row_stride, q_rotated ? nullptr : bt.cos_tab,
+                             q_rotated ? nullptr : bt.sin_tab, bt.seq_lens, bt.max_seq_len,
+                             layer.view, layer.window, layer.sinks, 0, bt.workspace,
+                             bt.workspace_bytes, out, out_stride, GKV_BF16, bt.dev_err),
+        "attention_bf16_chunk64");
+}
+
+// The exact path's fp32-output attention (attention_exact,
+// getp-csrc/kernels/attention.hpp:18-83), same arguments, fp32 [B][out_stride].
+inline void attention_exact(stream_t s, const float *qkv, int row_stride,
+                            const PagedLayer &layer, int n_q_heads, float *out, int out_stride,
+                            int B, const PagedBatch &bt, bool q_rotated = false) {
+  check(gkv_decode_attention(s, B, n_q_heads, qkv, row_stride, q_rotated ? nullptr : bt.cos_tab,
+                             q_rotated ? nullptr : bt.sin_tab, bt.seq_lens, bt.max_seq_len,
+                             layer.view, layer.window, layer.sinks, 0, bt.workspace,
+                             bt.workspace_bytes, out, out_stride, GKV_F32, bt.dev_err),
+        "attention_exact");
+}
+
+} // namespace gkv_engine
+
+#endif // GKV_ENGINE_HPP

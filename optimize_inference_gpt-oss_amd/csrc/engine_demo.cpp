@@ -1,0 +1,137 @@
+// A decode loop written the way the reference engine drives its attention
+// (layer_attention, getp-csrc/engine/gpu_engine.hpp:467-508, one position for
+// the whole batch per step), but through the C++ engine shim over the paged
+// pool: per step, reserve the new position of every sequence, upload the
+// tables, then per layer rope_kv_bf16(rotate_q = false) and
+// attention_bf16_chunk64 with the query rotated on load.
+//
+//   gkv_engine_demo <in.bin> <out.bin>
+// in.bin:  int32 P, B, Hq, Hkv, n_layers, window; fp32 qkv [P][n_layers][B][(Hq+2Hkv)*64];
+//          fp32 sinks [n_layers][Hq]
+// out.bin: bf16 [P][n_layers][B][Hq*64] attention outputs of every step
+// Layer l is a window layer iff window > 0 and l is even (the pool's rule).
+#include <hip/hip_runtime_api.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+#include "gkv_engine.hpp"
+
+#define HIP_OK(x)                                                                                \
+  do {                                                                                           \
+    hipError_t e_ = (x);                                                                         \
+    if (e_ != hipSuccess) {                                                                      \
+      fprintf(stderr, "%s: %s\n", #x, hipGetErrorString(e_));                                    \
+      return 1;                                                                                  \
+    }                                                                                            \
+  } while (0)
+
+int main(int argc, char **argv) {
+  if (argc != 3) {
+    fprintf(stderr, "usage: %s in.bin out.bin\n", argv[0]);
+    return 2;
+  }
+  FILE *f = fopen(argv[1], "rb");
+  if (!f)
+    return 2;
+  int32_t hdr[6];
+  if (fread(hdr, 4, 6, f) != 6)
+    return 2;
+  const int P = hdr[0], B = hdr[1], Hq = hdr[2], Hkv = hdr[3], NL = hdr[4], W = hdr[5];
+  const int QKV = (Hq + 2 * Hkv) * 64, ATT = Hq * 64;
+  std::vector<float> qkv((size_t)P * NL * B * QKV), sinks((size_t)NL * Hq);
+  if (fread(qkv.data(), 4, qkv.size(), f) != qkv.size() ||
+      fread(sinks.data(), 4, sinks.size(), f) != sinks.size())
+    return 2;
+  fclose(f);
+
+  gkv_pool_config cfg{};
+  cfg.n_layers = NL;
+  cfg.n_kv_heads = Hkv;
+  cfg.head_dim = 64;
+  cfg.window = W;
+  cfg.max_seqs = B;
+  cfg.max_seq_len = P;
+  cfg.num_blocks = (int64_t)B * ((P + 15) / 16) + 3;
+  cfg.shuffle_seed = 77;
+  gkv_pool *pool = nullptr;
+  gkv_engine::check(gkv_pool_create(&cfg, &pool), "gkv_pool_create");
+  for (int b = 0; b < B; b++) {
+    int32_t id = -1;
+    gkv_engine::check(gkv_pool_seq_alloc(pool, &id), "gkv_pool_seq_alloc");
+  }
+
+  std::vector<float> cos_h((size_t)P * 32), sin_h((size_t)P * 32);
+  gkv_rope_config rc{150000.0f, 64, 32.0f, 4096.0f, 32.0f, 1.0f}; // gpt-oss YaRN settings
+  gkv_engine::check(gkv_rope_table(&rc, P, cos_h.data(), sin_h.data()), "gkv_rope_table");
+
+  hipStream_t s;
+  HIP_OK(hipStreamCreate(&s));
+  float *d_qkv, *d_sinks, *d_cos, *d_sin;
+  int32_t *d_pos, *d_lens;
+  uint32_t *d_err;
+  uint16_t *d_out;
+  const size_t ws_bytes = gkv_decode_workspace_bytes(B, Hkv, P, 0, 0);
+  void *d_ws;
+  HIP_OK(hipMalloc(&d_qkv, (size_t)B * QKV * 4));
+  HIP_OK(hipMalloc(&d_sinks, sinks.size() * 4));
+  HIP_OK(hipMalloc(&d_cos, cos_h.size() * 4));
+  HIP_OK(hipMalloc(&d_sin, sin_h.size() * 4));
+  HIP_OK(hipMalloc(&d_pos, B * 4));
+  HIP_OK(hipMalloc(&d_lens, B * 4));
+  HIP_OK(hipMalloc(&d_err, 4));
+  HIP_OK(hipMalloc(&d_out, (size_t)B * ATT * 2));
+  HIP_OK(hipMalloc(&d_ws, ws_bytes));
+  HIP_OK(hipMemcpy(d_sinks, sinks.data(), sinks.size() * 4, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(d_cos, cos_h.data(), cos_h.size() * 4, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(d_sin, sin_h.data(), sin_h.size() * 4, hipMemcpyHostToDevice));
+  HIP_OK(hipMemset(d_err, 0, 4));
+
+  std::vector<gkv_engine::PagedLayer> layers(NL);
+  for (int l = 0; l < NL; l++) {
+    gkv_engine::check(gkv_pool_layer_view(pool, l, &layers[l].view), "gkv_pool_layer_view");
+    layers[l].window = layers[l].view.ring;
+    layers[l].sinks = d_sinks + (size_t)l * Hq;
+  }
+  gkv_engine::PagedBatch bt{d_pos, d_lens, P, d_cos, d_sin, d_ws, ws_bytes, d_err};
+
+  std::vector<uint16_t> out((size_t)P * NL * B * ATT);
+  std::vector<int32_t> pos(B), lens(B);
+  for (int p = 0; p < P; p++) {
+    for (int b = 0; b < B; b++) {
+      pos[b] = p;
+      lens[b] = p + 1;
+      gkv_engine::check(gkv_pool_seq_reserve(pool, b, p + 1), "gkv_pool_seq_reserve");
+    }
+    gkv_engine::check(gkv_pool_sync(pool, s), "gkv_pool_sync");
+    HIP_OK(hipMemcpyAsync(d_pos, pos.data(), B * 4, hipMemcpyHostToDevice, s));
+    HIP_OK(hipMemcpyAsync(d_lens, lens.data(), B * 4, hipMemcpyHostToDevice, s));
+    for (int l = 0; l < NL; l++) {
+      HIP_OK(hipMemcpyAsync(d_qkv, qkv.data() + ((size_t)p * NL + l) * B * QKV,
+                            (size_t)B * QKV * 4, hipMemcpyHostToDevice, s));
+      gkv_engine::rope_kv_bf16(s, B, d_qkv, QKV, bt, Hq, layers[l], /*rotate_q=*/false);
+      gkv_engine::attention_bf16_chunk64(s, d_qkv, QKV, layers[l], Hq, d_out, ATT, B, bt);
+      HIP_OK(hipMemcpyAsync(out.data() + ((size_t)p * NL + l) * B * ATT, d_out,
+                            (size_t)B * ATT * 2, hipMemcpyDeviceToHost, s));
+      HIP_OK(hipStreamSynchronize(s));
+    }
+  }
+  uint32_t err = 0;
+  HIP_OK(hipMemcpy(&err, d_err, 4, hipMemcpyDeviceToHost));
+  if (err) {
+    fprintf(stderr, "device error word %u\n", err);
+    return 1;
+  }
+  FILE *g = fopen(argv[2], "wb");
+  if (!g || fwrite(out.data(), 2, out.size(), g) != out.size())
+    return 2;
+  fclose(g);
+  gkv_pool_destroy(pool);
+  for (void *ptr : {(void *)d_qkv, (void *)d_sinks, (void *)d_cos, (void *)d_sin, (void *)d_pos,
+                    (void *)d_lens, (void *)d_err, (void *)d_out, d_ws})
+    (void)hipFree(ptr);
+  (void)hipStreamDestroy(s);
+  printf("engine demo: %d steps x %d layers x %d sequences ok\n", P, NL, B);
+  return 0;
+}

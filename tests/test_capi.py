@@ -126,3 +126,21 @@ def test_workspace_formula(gkv):
     assert gkv.workspace_bytes(B, hkv, 2049) == fixed + (B + 2048) * hkv * (512 + 16) * 4
     # a window layer bounds the stream by the window
     assert gkv.workspace_bytes(B, hkv, 100000, window=128) == gkv.workspace_bytes(B, hkv, 128)
+
+
+def test_engine_shim_header_compiles(tmp_path):
+    """The C++ shim header parses as host C++ against gkv.h (no GPU needed)."""
+    import shutil
+    import subprocess
+    cxx = shutil.which("g++")
+    if cxx is None:
+        import pytest
+        pytest.skip("no g++")
+    src = tmp_path / "shim.cpp"
+    src.write_text('#include "gkv_engine.hpp"\nint main() { gkv_engine::PagedBatch b{}; '
+                   'gkv_engine::PagedLayer l{}; (void)b; (void)l; return 0; }\n')
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([cxx, "-std=c++17", "-fsyntax-only", "-Wall", "-Werror",
+                        "-I", os.path.join(root, "include"), str(src)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

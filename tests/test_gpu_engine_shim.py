@@ -1,0 +1,52 @@
+"""The C++ engine shim (include/gkv_engine.hpp) driven the way the reference
+engine drives its attention: a C++ decode loop (csrc/engine_demo.cpp, built by
+build()) calls rope_kv_bf16 + attention_bf16_chunk64 per layer and step over
+the paged pool (one window layer with a wrapping 32-slot ring, one full
+layer). Every step's bf16 output is compared with the CPU oracle, which keeps
+the history by position: max-abs 2e-3 + rel 1e-2, plus bf16 output rounding.
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from kvcase import allclose_report
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+DEMO = os.path.join(ROOT, "optimize_inference_gpt-oss_amd", "gkv_engine_demo")
+
+
+def test_engine_shim_decode_loop(oracle, cuda, tmp_path):
+    if not os.path.exists(DEMO):
+        pytest.fail("gkv_engine_demo is not built (run __graft_entry__.build())")
+    P, B, Hq, Hkv, NL, W = 40, 3, 64, 8, 2, 32
+    rng = np.random.default_rng(2024)
+    qkv = (rng.standard_normal((P, NL, B, (Hq + 2 * Hkv) * 64)) * 0.5).astype(np.float32)
+    sinks = rng.standard_normal((NL, Hq)).astype(np.float32)
+    inp, outp = tmp_path / "in.bin", tmp_path / "out.bin"
+    with open(inp, "wb") as f:
+        np.array([P, B, Hq, Hkv, NL, W], np.int32).tofile(f)
+        qkv.tofile(f)
+        sinks.tofile(f)
+    r = subprocess.run([DEMO, str(inp), str(outp)], capture_output=True, text=True, timeout=90)
+    assert r.returncode == 0, r.stderr
+    got = np.fromfile(outp, np.uint16).reshape(P, NL, B, Hq, 64)
+    got = oracle.from_bf16(got)
+
+    cos, sin = oracle.rope_table(P)
+    for l in range(NL):
+        window = W if l % 2 == 0 else 0
+        kc = np.zeros((B, P, Hkv, 64), np.float32)
+        vc = np.zeros((B, P, Hkv, 64), np.float32)
+        for p in range(P):
+            pos = np.full(B, p, np.int32)
+            q_rot, _, kb, vb = oracle.kv_append(qkv[p, l], Hq, Hkv, cos, sin, pos)
+            kc[:, p] = oracle.from_bf16(kb)
+            vc[:, p] = oracle.from_bf16(vb)
+            ref = oracle.decode_attention(q_rot, kc[:, :p + 1], vc[:, :p + 1], pos, sinks[l],
+                                          window=window)
+            n_bad, max_err = allclose_report(got[p, l], ref, 2e-3, 1e-2 + 2 ** -8)
+            assert n_bad == 0, f"layer {l} step {p}: {n_bad} bad, max err {max_err}"
