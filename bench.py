@@ -319,6 +319,9 @@ def main() -> int:
     ap.add_argument("--lengths", default="random", choices=["random", "sorted", "fixed"],
                     help="diagnostics: context lengths in batch order as drawn, sorted "
                          "longest first, or all equal to the mean")
+    ap.add_argument("--separate-append", action="store_true",
+                    help="append with gkv_kv_append, then gkv_decode_attention (four launches "
+                         "per layer instead of gkv_decode_layer's three)")
     ap.add_argument("--sequential-blocks", action="store_true",
                     help="diagnostics: hand out physical blocks in id order (no shuffle)")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -382,22 +385,31 @@ def main() -> int:
 
     ev = {}
 
+    # A step: per layer, the append of every sequence's new token and the
+    # attention. Default: gkv_decode_layer's three launches (append fused with
+    # the prepare launch, split, combine); --separate-append: gkv_kv_append then
+    # gkv_decode_attention's three launches.
+    stages = ("append", "prepare", "split", "combine") if args.separate_append else \
+        ("append+prepare", "split", "combine")
+
     def step(record: bool):
         for li, layer in enumerate(layers):
-            e = [torch.cuda.Event(enable_timing=True) for _ in range(5)] if record else None
-            if record:
-                e[0].record(stream)
-            gkv.kv_append(layer.qkv, Hq, cos_d, sin_d, pos_d, layer.view, seq_lens=lens_d,
-                          dev_err=err_d, stream=stream)
-            for i, stage in enumerate(("prepare", "split", "combine")):
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] \
+                if record else None
+            for i, stage in enumerate(stages):
                 if record:
-                    e[i + 1].record(stream)
+                    e[i].record(stream)
+                if stage == "append":
+                    gkv.kv_append(layer.qkv, Hq, cos_d, sin_d, pos_d, layer.view,
+                                  seq_lens=lens_d, dev_err=err_d, stream=stream)
+                    continue
+                api = {"append+prepare": "layer_prepare"}.get(stage, stage)
                 gkv.decode_attention(layer.qkv, lens_d, max_len, layer.view, layer.sinks,
                                      layer.out, window=layer.window, cos_tab=cos_d,
                                      sin_tab=sin_d, split_tokens=args.split_tokens, workspace=ws,
-                                     dev_err=err_d, stream=stream, stage=stage)
+                                     dev_err=err_d, stream=stream, stage=api)
             if record:
-                e[4].record(stream)
+                e[-1].record(stream)
                 ev.setdefault(li, []).append(e)
 
     for _ in range(args.warmup):
@@ -423,13 +435,16 @@ def main() -> int:
     for _ in range(args.steps):
         step(True)
     torch.cuda.synchronize()
-    stage_ms = np.zeros(4)  # append, prepare, split, combine (summed over layers)
+    n_st = len(stages)
+    stage_ms = np.zeros(n_st)  # per stage, summed over layers
     for li, lst in ev.items():
-        stage_ms += [np.mean([e[i].elapsed_time(e[i + 1]) for e in lst]) for i in range(4)]
+        stage_ms += [np.mean([e[i].elapsed_time(e[i + 1]) for e in lst]) for i in range(n_st)]
     # dominant kernel: the split kernel of the full-attention layers (or of the
     # window layers when there are no full ones)
+    isp = stages.index("split")
     full = [i for i, l in enumerate(layers) if not l.window] or list(range(len(layers)))
-    dom_ms = float(np.mean([np.mean([e[2].elapsed_time(e[3]) for e in ev[i]]) for i in full]))
+    dom_ms = float(np.mean([np.mean([e[isp].elapsed_time(e[isp + 1]) for e in ev[i]])
+                            for i in full]))
     dom_bytes = float(np.mean([bytes_of(layers[i]) for i in full]))
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
 
@@ -466,8 +481,7 @@ def main() -> int:
             "context": f"U[{cfg['lo']},{cfg['hi']}]", "window": cfg["window"],
             "kv_bytes_per_step": kv_bytes, "split_tokens": args.split_tokens or 512,
             "pool_bytes": pool.device_bytes(),
-            "kernel_ms": dict(zip(("append", "prepare", "split", "combine"),
-                                  (round(float(x), 4) for x in stage_ms))),
+            "kernel_ms": dict(zip(stages, (round(float(x), 4) for x in stage_ms))),
             "parallelism": "1 GPU",
         },
         "roofline": {

@@ -14,6 +14,8 @@
  *                            (and rope_exact + kv_write_kernel, kernels/misc.hpp:55-85)
  *   gkv_decode_attention  <- attention_q8v_chunk64 / attention_bf16_chunk64 / attention_bf16,
  *                            getp-csrc/kernels/fast_attention.hpp:604-622, 566-580, 525-547
+ *   gkv_decode_layer      <- the pair rope_kv_bf16 + attention_q8v_chunk64 in layer_attention,
+ *                            getp-csrc/engine/gpu_engine.hpp:495-498 (one call, fused first launch)
  *   gkv_decode_prepare, gkv_decode_split, gkv_decode_combine
  *                         <- the per-wave split and the LDS merge inside
  *                            attention_gqa8_kernel, fast_attention.hpp:164-425 (a7: 383-424)
@@ -165,6 +167,28 @@ int gkv_decode_combine(void *stream, int32_t B, int32_t n_q_heads, int32_t n_kv_
                        const int32_t *seq_lens, int32_t max_seq_len, int32_t window,
                        const float *sinks, int32_t split_tokens, const void *workspace,
                        size_t workspace_bytes, void *out, int64_t out_stride, int32_t out_dtype);
+
+/* One decode layer in one call: the append of every sequence's new token
+ * and the attention, replacing the pair rope_kv_bf16 + attention_q8v_chunk64
+ * of layer_attention (getp-csrc/engine/gpu_engine.hpp:495-498). Row b of qkv
+ * ([Q | K | V] fp32, not rotated) is the new token of sequence b at position
+ * seq_lens[b] - 1; its K (rotated) and V go into the cache, then the
+ * attention runs as gkv_decode_attention with q = qkv, q_stride = row_stride
+ * (cos_tab/sin_tab required). gkv_decode_layer_prepare is its first launch
+ * (the append fused with gkv_decode_prepare); gkv_decode_split and
+ * gkv_decode_combine with the same arguments (q = qkv) complete it. */
+int gkv_decode_layer(void *stream, int32_t B, int32_t n_q_heads, const float *qkv,
+                     int64_t row_stride, const float *cos_tab, const float *sin_tab,
+                     const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,
+                     int32_t window, const float *sinks, int32_t split_tokens, void *workspace,
+                     size_t workspace_bytes, void *out, int64_t out_stride, int32_t out_dtype,
+                     uint32_t *dev_err);
+int gkv_decode_layer_prepare(void *stream, int32_t B, int32_t n_q_heads, const float *qkv,
+                             int64_t row_stride, const float *cos_tab, const float *sin_tab,
+                             const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,
+                             int32_t window, const float *sinks, int32_t split_tokens,
+                             void *workspace, size_t workspace_bytes, void *out,
+                             int64_t out_stride, int32_t out_dtype, uint32_t *dev_err);
 
 /* ---- Prefill (causal) attention ----------------------------------------- */
 

@@ -54,7 +54,7 @@
 // leaves the younger ones running alone at the end). Every load is
 // unconditional (indices are clamped), so the compiler's wait counts are
 // exact and a step never waits for the prefetches issued after it.
-#include "gkv_device.hpp"
+#include "kv_append.hpp"
 
 #include <algorithm>
 #include <cstdlib>
@@ -70,9 +70,19 @@ constexpr int kPlanHeader = 4;         // ints: T, S, workgroups used, unused
 constexpr int kIdRegs = 4;             // block-id registers per wave: ranges of <= 4096 tokens
 constexpr int kMaxRange = kIdRegs * 64 * kBlockTokens;
 constexpr int kInfoRegs = kMaxRange / kStep / 64; // step-record registers
-constexpr int kSplitThreads = 256;     // split kernel: 4 waves, one per SIMD
+#ifndef GKV_SPLIT_WAVES
+#define GKV_SPLIT_WAVES 4
+#endif
+constexpr int kSplitWaves = GKV_SPLIT_WAVES; // split kernel: waves per workgroup (4: one per SIMD)
+constexpr int kSplitThreads = 64 * kSplitWaves;
 constexpr int kPrepThreads = 1024;
 constexpr int kMaxBatch = 8192;        // sequences per call (prefix sums kept in LDS)
+// Query operands are loaded only with the step that opens a segment (true), or
+// with every step (false).
+#ifndef GKV_Q_AT_SEGMENT_START
+#define GKV_Q_AT_SEGMENT_START 1
+#endif
+constexpr bool kQAtSegmentStart = GKV_Q_AT_SEGMENT_START;
 constexpr int kBadBlock = -1;          // F entry: id outside the pool
 constexpr int kPadBlock = -2;          // F entry: no tokens (padding)
 
@@ -185,8 +195,9 @@ __device__ void prep_queries(const DecodeArgs &a, int item) {
 
 // Every workgroup computes the prefix sums in LDS (the lengths are 4 bytes per
 // sequence, cheap to read again), then takes its share of the stream blocks
-// and of the query items; workgroup 0 also publishes the plan.
-__global__ __launch_bounds__(kPrepThreads) void decode_prep_kernel(DecodeArgs a) {
+// and of the query items; workgroup 0 also publishes the plan. wg / n_wgs:
+// this workgroup's index among the prep workgroups and their count.
+__device__ __forceinline__ void prep_body(const DecodeArgs &a, int wg, int n_wgs) {
   __shared__ int s_cu[kMaxBatch + 1];
   __shared__ int s_scan[2][kPrepThreads];
   const int t = threadIdx.x, B = a.B;
@@ -202,7 +213,7 @@ __global__ __launch_bounds__(kPrepThreads) void decode_prep_kernel(DecodeArgs a)
       any_over |= over;
     }
   }
-  if (any_over && blockIdx.x == 0 && a.dev_err)
+  if (any_over && wg == 0 && a.dev_err)
     atomicOr(a.dev_err, GKV_DEVERR_LENGTH);
   // inclusive scan of the per-thread sums (Hillis-Steele, double buffered)
   int buf = 0;
@@ -229,7 +240,7 @@ __global__ __launch_bounds__(kPrepThreads) void decode_prep_kernel(DecodeArgs a)
   int S = a.fixed_S;
   if (S == 0)
     S = max(kStep, pad_step((T + a.n_wg - 1) / a.n_wg));
-  if (blockIdx.x == 0) {
+  if (wg == 0) {
     int32_t *cu = a.plan + kPlanHeader;
     for (int b = t; b <= B; b += kPrepThreads)
       cu[b] = s_cu[b];
@@ -243,7 +254,7 @@ __global__ __launch_bounds__(kPrepThreads) void decode_prep_kernel(DecodeArgs a)
   // Stream blocks (and the step records at even blocks), grid-strided.
   bool any_bad = false;
   const int n_e = T / kBlockTokens;
-  for (int e = blockIdx.x * kPrepThreads + t; e < n_e; e += gridDim.x * kPrepThreads) {
+  for (int e = wg * kPrepThreads + t; e < n_e; e += n_wgs * kPrepThreads) {
     const int tok = e * kBlockTokens;
     int lo = 0, hi = B - 1; // the sequence holding the block: last b with cu[b] <= tok
     while (lo < hi) {
@@ -274,9 +285,31 @@ __global__ __launch_bounds__(kPrepThreads) void decode_prep_kernel(DecodeArgs a)
 
   // Query operands: one wave per (sequence, kv head).
   const int waves = kPrepThreads / 64;
-  for (int item = blockIdx.x * waves + (t >> 6); item < B * a.n_kv_heads;
-       item += gridDim.x * waves)
+  for (int item = wg * waves + (t >> 6); item < B * a.n_kv_heads; item += n_wgs * waves)
     prep_queries(a, item);
+}
+
+__global__ __launch_bounds__(kPrepThreads) void decode_prep_kernel(DecodeArgs a) {
+  prep_body(a, blockIdx.x, gridDim.x);
+}
+
+// The append of a decode layer (row b = the new token of sequence b, at
+// position seq_lens[b] - 1) and the prepare work in one launch: workgroups
+// 0 .. n_app-1 append 4 rows each (256 threads per row), the others run
+// prep_body. The two parts touch disjoint memory (the prepare reads the raw
+// query of the qkv rows, the block tables and the lengths).
+constexpr int kAppendRowsPerWg = kPrepThreads / 256;
+__global__ __launch_bounds__(kPrepThreads) void decode_layer_prep_kernel(DecodeArgs a,
+                                                                         AppendArgs ap,
+                                                                         int n_rows,
+                                                                         int n_app) {
+  if ((int)blockIdx.x < n_app) {
+    const int r = blockIdx.x * kAppendRowsPerWg + (threadIdx.x >> 8);
+    if (r < n_rows)
+      append_row(ap, r, threadIdx.x & 255, 256);
+    return;
+  }
+  prep_body(a, blockIdx.x - n_app, gridDim.x - n_app);
 }
 
 // ---- split ----------------------------------------------------------------------
@@ -284,7 +317,7 @@ __global__ __launch_bounds__(kPrepThreads) void decode_prep_kernel(DecodeArgs a)
 // R: depth of the register ring of loaded steps (R - 1 steps in flight ahead
 // of the one being computed).
 template <int R>
-__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(1)))
+__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(kSplitWaves / 4)))
 void decode_split_kernel(DecodeArgs a) {
   constexpr int D = kHeadDim;
   const int w_id = blockIdx.x;
@@ -327,207 +360,232 @@ void decode_split_kernel(DecodeArgs a) {
     return v;
   };
 
-  // One wave per SIMD; wave wv works on kv heads wv, wv + n_waves, ... in
-  // turn, each over the whole range.
-  for (int g = wv; g < a.n_kv_heads; g += n_waves) {
-    // Ring slot: K (4 x 16 B per lane), V (4 x 16 B), the step's query
-    // operands (2 x 16 B), and its record with the bad-block bits.
-    u32x4 kbuf[R][4], vbuf[R][4], qbuf[R][2];
-    int rec[R], badb[R];
-    auto load_step = [&](int step, u32x4 (&kr)[4], u32x4 (&vr)[4], u32x4 (&qr)[2], int &rc,
-                         int &bb) {
-      int p0 = pick(tv, kIdRegs, 2 * step), p1 = pick(tv, kIdRegs, 2 * step + 1);
-      rc = pick(ti, kInfoRegs, step);
-      // a bad id masks its block like padding (bit jt per block)
-      bb = (p0 == kBadBlock ? 1 : 0) | (p1 == kBadBlock ? 2 : 0);
-      p0 = max(p0, 0);
-      p1 = max(p1, 0);
-      const size_t h0 = ((size_t)p0 * a.n_kv_heads + g) * head_bytes;
-      const size_t h1 = ((size_t)p1 * a.n_kv_heads + g) * head_bytes;
-      const __amdgpu_buffer_rsrc_t k0 = head_rsrc((const char *)a.kc + h0);
-      const __amdgpu_buffer_rsrc_t k1 = head_rsrc((const char *)a.kc + h1);
-      const __amdgpu_buffer_rsrc_t v0 = head_rsrc((const char *)a.vc + h0);
-      const __amdgpu_buffer_rsrc_t v1 = head_rsrc((const char *)a.vc + h1);
-      kr[0] = __builtin_amdgcn_raw_buffer_load_b128(k0, k_off, 0, 0);
-      kr[1] = __builtin_amdgcn_raw_buffer_load_b128(k0, k_off + 64, 0, 0);
-      kr[2] = __builtin_amdgcn_raw_buffer_load_b128(k1, k_off, 0, 0);
-      kr[3] = __builtin_amdgcn_raw_buffer_load_b128(k1, k_off + 64, 0, 0);
+  // One wave per SIMD. Wave wv takes kv heads wv and wv + n_waves (at most two
+  // passes over the range: Hkv <= 8 and n_waves = min(4, Hkv)). The passes form
+  // one stream of virtual steps v = pass * n_steps + step, so the load ring runs
+  // on across the change of head as it does across sequences.
+  const int n_passes = (a.n_kv_heads - wv + n_waves - 1) / n_waves; // 1 or 2
+  const int last_v = n_passes * n_steps - 1;
+  float sink_p[2];
 #pragma unroll
-      for (int nn = 0; nn < 4; nn++) {
-        const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(v0, v_off + nn * 512, 0, 0);
-        const u32x2 y = __builtin_amdgcn_raw_buffer_load_b64(v1, v_off + nn * 512, 0, 0);
-        vr[nn] = u32x4{x[0], x[1], y[0], y[1]};
-      }
+  for (int pp = 0; pp < 2; pp++) {
+    const int gp = min(wv + pp * n_waves, a.n_kv_heads - 1);
+    sink_p[pp] = head_ok ? a.sinks[gp * a.G + head] * kLog2e : 0.0f;
+  }
+
+  // Ring slot: K (4 x 16 B per lane), V (4 x 16 B), the query operands
+  // (2 x 16 B; loaded only for a step that opens a segment), the step record,
+  // and the bad-block bits | pass << 2.
+  u32x4 kbuf[R][4], vbuf[R][4], qbuf[R][2];
+  int rec[R], badb[R];
+  auto load_step = [&](int v, u32x4 (&kr)[4], u32x4 (&vr)[4], u32x4 (&qr)[2], int &rc,
+                       int &bb) {
+    const int pass = v >= n_steps ? 1 : 0;
+    const int step = v - pass * n_steps;
+    const int g = wv + pass * n_waves;
+    int p0 = pick(tv, kIdRegs, 2 * step), p1 = pick(tv, kIdRegs, 2 * step + 1);
+    rc = pick(ti, kInfoRegs, step);
+    // a bad id masks its block like padding (bit jt per block)
+    bb = (p0 == kBadBlock ? 1 : 0) | (p1 == kBadBlock ? 2 : 0) | (pass << 2);
+    p0 = max(p0, 0);
+    p1 = max(p1, 0);
+    const size_t h0 = ((size_t)p0 * a.n_kv_heads + g) * head_bytes;
+    const size_t h1 = ((size_t)p1 * a.n_kv_heads + g) * head_bytes;
+    const __amdgpu_buffer_rsrc_t k0 = head_rsrc((const char *)a.kc + h0);
+    const __amdgpu_buffer_rsrc_t k1 = head_rsrc((const char *)a.kc + h1);
+    const __amdgpu_buffer_rsrc_t v0 = head_rsrc((const char *)a.vc + h0);
+    const __amdgpu_buffer_rsrc_t v1 = head_rsrc((const char *)a.vc + h1);
+    kr[0] = __builtin_amdgcn_raw_buffer_load_b128(k0, k_off, 0, 0);
+    kr[1] = __builtin_amdgcn_raw_buffer_load_b128(k0, k_off + 64, 0, 0);
+    kr[2] = __builtin_amdgcn_raw_buffer_load_b128(k1, k_off, 0, 0);
+    kr[3] = __builtin_amdgcn_raw_buffer_load_b128(k1, k_off + 64, 0, 0);
+#pragma unroll
+    for (int nn = 0; nn < 4; nn++) {
+      const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(v0, v_off + nn * 512, 0, 0);
+      const u32x2 y = __builtin_amdgcn_raw_buffer_load_b64(v1, v_off + nn * 512, 0, 0);
+      vr[nn] = u32x4{x[0], x[1], y[0], y[1]};
+    }
+    if (!kQAtSegmentStart || (rc & 0x80) || step == 0) {
       const u32x4 *qs = a.qops + (((int64_t)(rc >> 8) * a.n_kv_heads + g) * 64 + lane) * 2;
       qr[0] = qs[0];
       qr[1] = qs[1];
-    };
+    }
+  };
 
-    // The ring's first loads go out before anything else.
-    const int last_step = n_steps - 1;
+  // The ring's first loads go out before anything else.
 #pragma unroll
-    for (int r = 0; r < R - 1; r++)
-      load_step(min(r, last_step), kbuf[r], vbuf[r], qbuf[r], rec[r], badb[r]);
+  for (int r = 0; r < R - 1; r++)
+    load_step(min(r, last_v), kbuf[r], vbuf[r], qbuf[r], rec[r], badb[r]);
 
-    const float sink2 = head_ok ? a.sinks[g * a.G + head] * kLog2e : 0.0f;
-    int cur_b = -1;             // sequence of the open segment (-1: none)
-    bool cur_whole = false;     // the segment began at its sequence's first step
-    bool cur_ends = false;      // ... and has reached its last step
-    float m_run = sink2;        // running reference max (log2 units) of this column
-    float lsum = 0.0f;
-    f32x4 o[4];
+  int cur_key = -1;           // sequence | pass << 16 of the open segment (-1: none)
+  int cur_b = 0, cur_g = 0;   // its sequence and kv head
+  float cur_sink = 0.0f;      // its sink (log2 units)
+  bool cur_whole = false;     // the segment began at its sequence's first step
+  bool cur_ends = false;      // ... and has reached its last step
+  float m_run = 0.0f;         // running reference max (log2 units) of this column
+  float lsum = 0.0f;
+  u32x4 qcur[2] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
+  f32x4 o[4];
+#pragma unroll
+  for (int nn = 0; nn < 4; nn++)
+    o[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // Finishes the open segment: the output (sink added) if it is the whole
+  // sequence, else the partial for the combine.
+  auto flush = [&]() {
+    float ls = lsum;
+    ls += __shfl_xor(ls, 16);
+    ls += __shfl_xor(ls, 32);
+    f32x4 oo[4];
 #pragma unroll
     for (int nn = 0; nn < 4; nn++)
-      o[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    // Finishes the open segment: the output (sink added) if it is the whole
-    // sequence, else the partial for the combine.
-    auto flush = [&]() {
-      float ls = lsum;
-      ls += __shfl_xor(ls, 16);
-      ls += __shfl_xor(ls, 32);
-      f32x4 oo[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        oo[nn][r] = o[nn][r] + swap8(o[nn][r]);
+    if (lo || !head_ok || cur_key < 0)
+      return;
+    const int hq = cur_g * a.G + head;
+    if (cur_whole && cur_ends) {
+      // out = o * 2^(m - M) / (l * 2^(m - M) + 2^(sink - M)), M = max(m, sink)
+      const float M2 = fmaxf(m_run, cur_sink);
+      const float f = __builtin_amdgcn_exp2f(m_run - M2);
+      const float scale = f / fmaf(ls, f, __builtin_amdgcn_exp2f(cur_sink - M2));
+      const int64_t ob = (int64_t)cur_b * a.out_stride + (int64_t)hq * D + 4 * kg;
+#pragma unroll
+      for (int nn = 0; nn < 4; nn++) {
+        if (a.out_bf16) {
+          typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+          *(bf16x4 *)((__bf16 *)a.out + ob + 16 * nn) =
+              bf16x4{(__bf16)(oo[nn][0] * scale), (__bf16)(oo[nn][1] * scale),
+                     (__bf16)(oo[nn][2] * scale), (__bf16)(oo[nn][3] * scale)};
+        } else {
+          *(f32x4 *)((float *)a.out + ob + 16 * nn) = oo[nn] * scale;
+        }
+      }
+    } else {
+      const int64_t part = ((int64_t)(cur_b + w_id)) * a.n_kv_heads + cur_g;
+      float *wo = a.ws_o + part * kPartFloats + head * D + 4 * kg;
 #pragma unroll
       for (int nn = 0; nn < 4; nn++)
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-          oo[nn][r] = o[nn][r] + swap8(o[nn][r]);
-      if (lo || !head_ok || cur_b < 0)
-        return;
-      const int hq = g * a.G + head;
-      if (cur_whole && cur_ends) {
-        // out = o * 2^(m - M) / (l * 2^(m - M) + 2^(sink - M)), M = max(m, sink)
-        const float M2 = fmaxf(m_run, sink2);
-        const float f = __builtin_amdgcn_exp2f(m_run - M2);
-        const float scale = f / fmaf(ls, f, __builtin_amdgcn_exp2f(sink2 - M2));
-        const int64_t ob = (int64_t)cur_b * a.out_stride + (int64_t)hq * D + 4 * kg;
-#pragma unroll
-        for (int nn = 0; nn < 4; nn++) {
-          if (a.out_bf16) {
-            typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-            *(bf16x4 *)((__bf16 *)a.out + ob + 16 * nn) =
-                bf16x4{(__bf16)(oo[nn][0] * scale), (__bf16)(oo[nn][1] * scale),
-                       (__bf16)(oo[nn][2] * scale), (__bf16)(oo[nn][3] * scale)};
-          } else {
-            *(f32x4 *)((float *)a.out + ob + 16 * nn) = oo[nn] * scale;
-          }
-        }
-      } else {
-        const int64_t part = ((int64_t)(cur_b + w_id)) * a.n_kv_heads + g;
-        float *wo = a.ws_o + part * kPartFloats + head * D + 4 * kg;
-#pragma unroll
-        for (int nn = 0; nn < 4; nn++)
-          *(f32x4 *)(wo + 16 * nn) = oo[nn];
-        if (kg == 0) {
-          a.ws_ml[part * kMlStride + 2 * head] = m_run;
-          a.ws_ml[part * kMlStride + 2 * head + 1] = ls;
-        }
-      }
-    };
-
-    auto compute_step = [&](u32x4 (&kr)[4], u32x4 (&vr)[4], u32x4 (&qr)[2], int rc, int bb,
-                            bool in_range) {
-      const int sb = rc >> 8;
-      if (in_range && sb != cur_b) {
-        // The step starts another sequence: flush, start a new segment.
-        flush();
-        cur_b = sb;
-        cur_whole = (rc & 0x80) != 0;
-        m_run = sink2;
-        lsum = 0.0f;
-#pragma unroll
-        for (int nn = 0; nn < 4; nn++)
-          o[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-      if (in_range)
-        cur_ends = (rc & 0x40) != 0;
-      const int valid = in_range ? (rc & 0x3f) : 0;
-      const uint32_t bad = (uint32_t)bb;
-      const bf16x8 qop0 = __builtin_bit_cast(bf16x8, qr[0]);
-      const bf16x8 qop1 = __builtin_bit_cast(bf16x8, qr[1]);
-      // Scores of token 4*kg + r of block jt (slot 4*jt + r), this lane's column.
-      float sc[8];
-#pragma unroll
-      for (int jt = 0; jt < 2; jt++) {
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * jt + 0]),
-                                                      qop0, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * jt + 1]),
-                                                      qop1, acc, 0, 0, 0);
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-          sc[4 * jt + r] = acc[r] + swap8(acc[r]);
-      }
-      if (valid < kStep || bad) {
-        // Tail of the sequence, padding, past the range, or a bad block id:
-        // those tokens get weight 0 and their values (possibly never written)
-        // become zeros.
-#pragma unroll
-        for (int jt = 0; jt < 2; jt++) {
-          const bool blk_bad = (bad >> jt) & 1;
-#pragma unroll
-          for (int r = 0; r < 4; r++)
-            if (16 * jt + 4 * kg + r >= valid || blk_bad)
-              sc[4 * jt + r] = -INFINITY;
-#pragma unroll
-          for (int h2 = 0; h2 < 2; h2++) {
-            const int tk = 16 * jt + 4 * kg + 2 * h2;
-            const uint32_t keep = blk_bad ? 0u
-                                          : ((tk < valid ? 0x0000ffffu : 0u) |
-                                             (tk + 1 < valid ? 0xffff0000u : 0u));
-#pragma unroll
-            for (int nn = 0; nn < 4; nn++)
-              vr[nn][2 * jt + h2] &= keep;
-          }
-        }
-      }
-
-      float mx = sc[0];
-#pragma unroll
-      for (int i = 1; i < 8; i++)
-        mx = fmaxf(mx, sc[i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      // Lazy rescale: the reference max moves only when a score exceeds it by
-      // more than 8 (weights stay below 2^8, harmless in fp32); the final
-      // normalisation uses the same max, so the result does not change.
-      if (__any(mx > m_run + 8.0f)) {
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
-        lsum *= alpha;
-#pragma unroll
-        for (int nn = 0; nn < 4; nn++)
-          o[nn] *= alpha;
-      }
-      float p[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        p[i] = __builtin_amdgcn_exp2f(sc[i] - m_run);
-        lsum += p[i];
-      }
-      const bf16x8 pop = pack_pieces(p, lo);
-#pragma unroll
-      for (int nn = 0; nn < 4; nn++)
-        o[nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vr[nn]), pop,
-                                                        o[nn], 0, 0, 0);
-    };
-
-    // Ring: slot r holds step base + r; the load for step + R - 1 goes out
-    // before step is computed. The step count is padded to a multiple of R;
-    // padded steps re-load the last step (cache hits) and are masked out.
-    for (int base = 0; base < n_steps; base += R) {
-#pragma unroll
-      for (int r = 0; r < R; r++) {
-        const int step = base + r;
-        const int slot = (r + R - 1) % R;
-        load_step(min(step + R - 1, last_step), kbuf[slot], vbuf[slot], qbuf[slot], rec[slot],
-                  badb[slot]);
-        compute_step(kbuf[r], vbuf[r], qbuf[r], rec[r], badb[r], step < n_steps);
+        *(f32x4 *)(wo + 16 * nn) = oo[nn];
+      if (kg == 0) {
+        a.ws_ml[part * kMlStride + 2 * head] = m_run;
+        a.ws_ml[part * kMlStride + 2 * head + 1] = ls;
       }
     }
-    flush();
-  } // kv heads
+  };
+
+  auto compute_step = [&](u32x4 (&kr)[4], u32x4 (&vr)[4], u32x4 (&qr)[2], int rc, int bb,
+                          bool in_range) {
+    const int pass = bb >> 2;
+    const int key = (rc >> 8) | (pass << 16);
+    if (in_range && key != cur_key) {
+      // The step opens another segment (new sequence or new head): flush,
+      // start over.
+      flush();
+      cur_key = key;
+      cur_b = rc >> 8;
+      cur_g = wv + pass * n_waves;
+      cur_sink = pass ? sink_p[1] : sink_p[0];
+      cur_whole = (rc & 0x80) != 0;
+      m_run = cur_sink;
+      lsum = 0.0f;
+#pragma unroll
+      for (int nn = 0; nn < 4; nn++)
+        o[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (kQAtSegmentStart) {
+        qcur[0] = qr[0];
+        qcur[1] = qr[1];
+      }
+    }
+    if (in_range)
+      cur_ends = (rc & 0x40) != 0;
+    const int valid = in_range ? (rc & 0x3f) : 0;
+    const uint32_t bad = (uint32_t)bb & 3u;
+    const bf16x8 qop0 = __builtin_bit_cast(bf16x8, kQAtSegmentStart ? qcur[0] : qr[0]);
+    const bf16x8 qop1 = __builtin_bit_cast(bf16x8, kQAtSegmentStart ? qcur[1] : qr[1]);
+    // Scores of token 4*kg + r of block jt (slot 4*jt + r), this lane's column.
+    float sc[8];
+#pragma unroll
+    for (int jt = 0; jt < 2; jt++) {
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * jt + 0]),
+                                                    qop0, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * jt + 1]),
+                                                    qop1, acc, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        sc[4 * jt + r] = acc[r] + swap8(acc[r]);
+    }
+    if (valid < kStep || bad) {
+      // Tail of the sequence, padding, past the range, or a bad block id:
+      // those tokens get weight 0 and their values (possibly never written)
+      // become zeros.
+#pragma unroll
+      for (int jt = 0; jt < 2; jt++) {
+        const bool blk_bad = (bad >> jt) & 1;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (16 * jt + 4 * kg + r >= valid || blk_bad)
+            sc[4 * jt + r] = -INFINITY;
+#pragma unroll
+        for (int h2 = 0; h2 < 2; h2++) {
+          const int tk = 16 * jt + 4 * kg + 2 * h2;
+          const uint32_t keep = blk_bad ? 0u
+                                        : ((tk < valid ? 0x0000ffffu : 0u) |
+                                           (tk + 1 < valid ? 0xffff0000u : 0u));
+#pragma unroll
+          for (int nn = 0; nn < 4; nn++)
+            vr[nn][2 * jt + h2] &= keep;
+        }
+      }
+    }
+
+    float mx = sc[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++)
+      mx = fmaxf(mx, sc[i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // Lazy rescale: the reference max moves only when a score exceeds it by
+    // more than 8 (weights stay below 2^8, harmless in fp32); the final
+    // normalisation uses the same max, so the result does not change.
+    if (__any(mx > m_run + 8.0f)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      lsum *= alpha;
+#pragma unroll
+      for (int nn = 0; nn < 4; nn++)
+        o[nn] *= alpha;
+    }
+    float p[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      p[i] = __builtin_amdgcn_exp2f(sc[i] - m_run);
+      lsum += p[i];
+    }
+    const bf16x8 pop = pack_pieces(p, lo);
+#pragma unroll
+    for (int nn = 0; nn < 4; nn++)
+      o[nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vr[nn]), pop,
+                                                      o[nn], 0, 0, 0);
+  };
+
+  // Ring: slot r holds virtual step base + r; the load for v + R - 1 goes out
+  // before v is computed. The count is padded to a multiple of R; padded
+  // steps re-load the last step (cache hits) and are masked out.
+  for (int base = 0; base <= last_v; base += R) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int v = base + r;
+      const int slot = (r + R - 1) % R;
+      load_step(min(v + R - 1, last_v), kbuf[slot], vbuf[slot], qbuf[slot], rec[slot],
+                badb[slot]);
+      compute_step(kbuf[r], vbuf[r], qbuf[r], rec[r], badb[r], v <= last_v);
+    }
+  }
+  flush();
 }
 
 // ---- combine --------------------------------------------------------------------
@@ -581,12 +639,12 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
 constexpr int kRing = 5;
 
 // Ring depth of the split kernel (default kRing; the tuning variable
-// GKV_DECODE_RING = 4..8 picks another, read once).
+// GKV_DECODE_RING = 3..8 picks another, read once).
 static int ring_depth() {
   static const int r = [] {
     const char *e = getenv("GKV_DECODE_RING");
     const int v = e ? atoi(e) : kRing;
-    return (v >= 4 && v <= 8) ? v : kRing;
+    return (v >= 3 && v <= 8) ? v : kRing;
   }();
   return r;
 }
@@ -598,6 +656,8 @@ static void launch_split_ring(const DecodeArgs &a, dim3 grid, dim3 block, hipStr
 
 static const void *split_kernel_fn(int ring) {
   switch (ring) {
+  case 3:
+    return (const void *)decode_split_kernel<3>;
   case 4:
     return (const void *)decode_split_kernel<4>;
   case 6:
@@ -611,7 +671,7 @@ static const void *split_kernel_fn(int ring) {
   }
 }
 
-static int split_block(int n_kv_heads) { return 64 * std::min(4, n_kv_heads); }
+static int split_block(int n_kv_heads) { return 64 * std::min(kSplitWaves, n_kv_heads); }
 
 // Workgroups the GPU holds at once for the split kernel (CUs x per-CU
 // occupancy), per device, measured once.
@@ -743,19 +803,33 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
   return GKV_OK;
 }
 
-static int launch_prep(const DecodeArgs &a, int64_t t_max, hipStream_t s) {
+static int prep_workgroups(const DecodeArgs &a, int64_t t_max) {
   const int waves = kPrepThreads / 64;
   const int64_t by_items = (a.B * a.n_kv_heads + waves - 1) / waves;
   const int64_t by_blocks = (t_max / kBlockTokens + kPrepThreads - 1) / kPrepThreads;
-  const int prep_wgs =
-      (int)std::max<int64_t>(1, std::min<int64_t>(1024, std::max(by_items, by_blocks)));
-  hipLaunchKernelGGL(decode_prep_kernel, dim3(prep_wgs), dim3(kPrepThreads), 0, s, a);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(1024, std::max(by_items, by_blocks)));
+}
+
+static int launch_prep(const DecodeArgs &a, int64_t t_max, hipStream_t s) {
+  hipLaunchKernelGGL(decode_prep_kernel, dim3(prep_workgroups(a, t_max)), dim3(kPrepThreads), 0,
+                     s, a);
   return launch_status("decode_prep_kernel");
+}
+
+static int launch_layer_prep(const DecodeArgs &a, const AppendArgs &ap, int64_t t_max,
+                             hipStream_t s) {
+  const int n_app = (a.B + kAppendRowsPerWg - 1) / kAppendRowsPerWg;
+  hipLaunchKernelGGL(decode_layer_prep_kernel, dim3(n_app + prep_workgroups(a, t_max)),
+                     dim3(kPrepThreads), 0, s, a, ap, a.B, n_app);
+  return launch_status("decode_layer_prep_kernel");
 }
 
 static int launch_split(const DecodeArgs &a, hipStream_t s) {
   const dim3 grid(a.n_wg), block(split_block(a.n_kv_heads));
   switch (ring_depth()) {
+  case 3:
+    launch_split_ring<3>(a, grid, block, s);
+    break;
   case 4:
     launch_split_ring<4>(a, grid, block, s);
     break;
@@ -793,6 +867,12 @@ extern "C" size_t gkv_decode_workspace_bytes(int32_t B, int32_t n_kv_heads, int3
 
 #define GKV_DECODE_PARAMS                                                                   \
   void *stream, int32_t B, int32_t n_q_heads, const float *q, int64_t q_stride,                \
+      const float *cos_tab, const float *sin_tab, const int32_t *seq_lens, int32_t max_seq_len, \
+      gkv_cache_view cache, int32_t window, const float *sinks, int32_t split_tokens,          \
+      void *workspace, size_t workspace_bytes_, void *out, int64_t out_stride,                  \
+      int32_t out_dtype, uint32_t *dev_err
+#define GKV_LAYER_PARAMS                                                                    \
+  void *stream, int32_t B, int32_t n_q_heads, const float *qkv, int64_t row_stride,            \
       const float *cos_tab, const float *sin_tab, const int32_t *seq_lens, int32_t max_seq_len, \
       gkv_cache_view cache, int32_t window, const float *sinks, int32_t split_tokens,          \
       void *workspace, size_t workspace_bytes_, void *out, int64_t out_stride,                  \
@@ -845,3 +925,65 @@ extern "C" int gkv_decode_attention(GKV_DECODE_PARAMS) {
     return st;
   return launch_combine(a, (hipStream_t)stream);
 }
+
+// ---- decode layer: append + attention -----------------------------------------
+
+static int layer_append_args(AppendArgs &ap, int32_t B, int32_t n_q_heads, const float *qkv,
+                             int64_t row_stride, const float *cos_tab, const float *sin_tab,
+                             const int32_t *seq_lens, const gkv_cache_view &cache,
+                             uint32_t *dev_err) {
+  if (!qkv || !cos_tab || !sin_tab || !cache.k || !cache.v)
+    return GKV_ERR_ARG;
+  if (row_stride < (int64_t)(n_q_heads + 2 * cache.n_kv_heads) * kHeadDim)
+    return GKV_ERR_ARG;
+  if (cache.ring % kBlockTokens != 0)
+    return GKV_ERR_UNSUPPORTED;
+  ap.qkv = qkv;
+  ap.row_stride = row_stride;
+  ap.n_q_heads = n_q_heads;
+  ap.n_kv_heads = cache.n_kv_heads;
+  ap.cos_tab = cos_tab;
+  ap.sin_tab = sin_tab;
+  ap.row_pos = nullptr; // position = seq_lens[b] - 1
+  ap.row_seq = nullptr;
+  ap.seq_lens = seq_lens;
+  ap.kc = (uint16_t *)cache.k;
+  ap.vc = (uint16_t *)cache.v;
+  ap.table = cache.block_table;
+  ap.table_stride = cache.table_stride;
+  ap.num_blocks = cache.num_blocks;
+  ap.ring = cache.ring;
+  ap.q_out = nullptr;
+  ap.q_out_stride = 0;
+  ap.k_pack = ap.v_pack = nullptr;
+  ap.dev_err = dev_err;
+  (void)B;
+  return GKV_OK;
+}
+
+#define GKV_LAYER_SETUP                                                                        \
+  DecodeArgs a;                                                                                \
+  AppendArgs ap;                                                                               \
+  int st = prepare(a, B, n_q_heads, qkv, row_stride, cos_tab, sin_tab, seq_lens, max_seq_len,  \
+                   cache, window, sinks, split_tokens, workspace, workspace_bytes_, out,       \
+                   out_stride, out_dtype, dev_err, true);                                     \
+  if (st == GKV_OK)                                                                            \
+    st = layer_append_args(ap, B, n_q_heads, qkv, row_stride, cos_tab, sin_tab, seq_lens,     \
+                           cache, dev_err);                                                    \
+  if (st != GKV_OK || B == 0)                                                                  \
+    return st;
+
+extern "C" int gkv_decode_layer_prepare(GKV_LAYER_PARAMS) {
+  GKV_LAYER_SETUP
+  return launch_layer_prep(a, ap, stream_max(B, max_seq_len, window), (hipStream_t)stream);
+}
+
+extern "C" int gkv_decode_layer(GKV_LAYER_PARAMS) {
+  GKV_LAYER_SETUP
+  if ((st = launch_layer_prep(a, ap, stream_max(B, max_seq_len, window), (hipStream_t)stream)))
+    return st;
+  if ((st = launch_split(a, (hipStream_t)stream)))
+    return st;
+  return launch_combine(a, (hipStream_t)stream);
+}
+

@@ -13,99 +13,12 @@
 // (V transposed inside its block so that the attention kernel's PV operand is
 // one 16-byte load per lane). One workgroup per row; HBM-bound and tiny
 // (2 KB written per token per layer).
-#include "gkv_device.hpp"
+#include "kv_append.hpp"
 
 namespace gkv {
 
-struct AppendArgs {
-  const float *qkv;
-  int64_t row_stride;
-  int n_q_heads, n_kv_heads;
-  const float *cos_tab, *sin_tab;
-  const int32_t *row_pos, *row_seq, *seq_lens;
-  uint16_t *kc, *vc;
-  const int32_t *table;
-  int table_stride, num_blocks, ring;
-  float *q_out;
-  int64_t q_out_stride;
-  uint16_t *k_pack, *v_pack;
-  uint32_t *dev_err;
-};
-
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
-  constexpr int D = kHeadDim, HALF = kHeadDim / 2;
-  const int r = blockIdx.x, tid = threadIdx.x;
-  const int pos = a.row_pos[r];
-  const int seq = a.row_seq ? a.row_seq[r] : r;
-  const float *row = a.qkv + (int64_t)r * a.row_stride;
-  const float *cs = a.cos_tab + (int64_t)pos * HALF, *sn = a.sin_tab + (int64_t)pos * HALF;
-  const int kv_dim = a.n_kv_heads * D;
-
-  // Rotated query (each thread owns whole pairs, so q_out may alias qkv).
-  if (a.q_out) {
-    float *qo = a.q_out + (int64_t)r * a.q_out_stride;
-    for (int idx = tid; idx < a.n_q_heads * HALF; idx += blockDim.x) {
-      const int h = idx / HALF, i = idx % HALF;
-      const float x1 = row[h * D + i], x2 = row[h * D + HALF + i];
-      const float c = cs[i], s = sn[i];
-      const float o1 = rope_first(x1, x2, c, s), o2 = rope_second(x1, x2, c, s);
-      qo[h * D + i] = o1;
-      qo[h * D + HALF + i] = o2;
-    }
-  }
-
-  // Where the token goes in the paged cache (if anywhere).
-  const int slot = a.ring > 0 ? pos % a.ring : pos;
-  bool store = a.kc != nullptr;
-  if (store && a.ring > 0 && a.seq_lens && pos + a.ring < a.seq_lens[seq])
-    store = false; // a later row of this call takes the ring slot
-  int64_t kbase = 0, vbase = 0;
-  const int off = slot % kBlockTokens;
-  if (store) {
-    const int blk = slot / kBlockTokens;
-    if (blk >= a.table_stride) {
-      if (tid == 0 && a.dev_err)
-        atomicOr(a.dev_err, GKV_DEVERR_LENGTH);
-      store = false;
-    } else {
-      const int phys = a.table[(int64_t)seq * a.table_stride + blk];
-      if (phys < 0 || phys >= a.num_blocks) {
-        if (tid == 0 && a.dev_err)
-          atomicOr(a.dev_err, GKV_DEVERR_BLOCK_ID);
-        store = false;
-      } else {
-        kbase = (int64_t)phys * a.n_kv_heads * (kBlockTokens * D);
-        vbase = kbase;
-      }
-    }
-  }
-
-  const float *kr = row + a.n_q_heads * D, *vr = kr + kv_dim;
-  for (int idx = tid; idx < a.n_kv_heads * HALF; idx += blockDim.x) {
-    const int g = idx / HALF, i = idx % HALF;
-    const float x1 = kr[g * D + i], x2 = kr[g * D + HALF + i];
-    const float c = cs[i], s = sn[i];
-    const uint16_t k1 = f32_to_bf16_rne(rope_first(x1, x2, c, s));
-    const uint16_t k2 = f32_to_bf16_rne(rope_second(x1, x2, c, s));
-    if (store) {
-      uint16_t *kd = a.kc + kbase + ((int64_t)g * kBlockTokens + off) * D;
-      kd[i] = k1;
-      kd[HALF + i] = k2;
-    }
-    if (a.k_pack) {
-      uint16_t *kp = a.k_pack + (int64_t)r * kv_dim + g * D;
-      kp[i] = k1;
-      kp[HALF + i] = k2;
-    }
-  }
-  for (int idx = tid; idx < kv_dim; idx += blockDim.x) {
-    const int g = idx / D, d = idx % D;
-    const uint16_t v = f32_to_bf16_rne(vr[idx]);
-    if (store)
-      a.vc[vbase + ((int64_t)g * D + d) * kBlockTokens + off] = v;
-    if (a.v_pack)
-      a.v_pack[(int64_t)r * kv_dim + idx] = v;
-  }
+  append_row(a, blockIdx.x, threadIdx.x, blockDim.x);
 }
 
 } // namespace gkv

@@ -67,6 +67,12 @@ SIGNATURES = {
     "gkv_decode_prepare": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
                                         CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
                                         _vp]),
+    "gkv_decode_layer": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
+                                        CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
+                                        _vp]),
+    "gkv_decode_layer_prepare": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
+                                        CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
+                                        _vp]),
     "gkv_decode_split": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
                                         CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
                                         _vp]),
@@ -205,12 +211,14 @@ def decode_attention(q, seq_lens, max_seq_len, view: CacheView, sinks, out, wind
     out_dtype = BF16 if out.dtype == torch.bfloat16 else F32
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     args_common = (stream_handle(stream), q.shape[0])
-    if stage in ("both", "prepare", "split"):
+    if stage in ("both", "prepare", "split", "layer", "layer_prepare"):
         name = {"both": "gkv_decode_attention", "prepare": "gkv_decode_prepare",
-                "split": "gkv_decode_split"}[stage]
-        st = getattr(lib(), name)(*args_common, sinks.shape[0], ptr(q), q.stride(0), ptr(cos_tab), ptr(sin_tab),
-                ptr(seq_lens), max_seq_len, view, window, ptr(sinks), split_tokens,
-                ptr(workspace), ws_bytes, ptr(out), out.stride(0), out_dtype, ptr(dev_err))
+                "split": "gkv_decode_split", "layer": "gkv_decode_layer",
+                "layer_prepare": "gkv_decode_layer_prepare"}[stage]
+        st = getattr(lib(), name)(*args_common, sinks.shape[0], ptr(q), q.stride(0),
+                                  ptr(cos_tab), ptr(sin_tab), ptr(seq_lens), max_seq_len, view,
+                                  window, ptr(sinks), split_tokens, ptr(workspace), ws_bytes,
+                                  ptr(out), out.stride(0), out_dtype, ptr(dev_err))
         check(name, st)
     if stage == "combine":
         st = lib().gkv_decode_combine(*args_common, sinks.shape[0], view.n_kv_heads,
@@ -218,6 +226,14 @@ def decode_attention(q, seq_lens, max_seq_len, view: CacheView, sinks, out, wind
                                       split_tokens, ptr(workspace), ws_bytes, ptr(out),
                                       out.stride(0), out_dtype)
         check("gkv_decode_combine", st)
+
+
+def decode_layer(qkv, seq_lens, max_seq_len, view: CacheView, sinks, out, cos_tab, sin_tab,
+                 window=0, split_tokens=0, workspace=None, dev_err=None, stream=None):
+    """gkv_decode_layer: append of row b at position seq_lens[b]-1, then attention."""
+    decode_attention(qkv, seq_lens, max_seq_len, view, sinks, out, window=window,
+                     cos_tab=cos_tab, sin_tab=sin_tab, split_tokens=split_tokens,
+                     workspace=workspace, dev_err=dev_err, stream=stream, stage="layer")
 
 
 def prefill_attention(cu_seqlens, max_len, q, k, v, sinks, out, n_kv_heads, window=0,

@@ -17,7 +17,7 @@ ATOL, RTOL = 2e-3, 1e-2
 
 
 def run_gpu(case: DecodeCase, gkv, torch, device, split_tokens=0, out_dtype=None,
-            rotate_in_attention=True, product_table=True):
+            rotate_in_attention=True, product_table=True, layer_call=False):
     cos = sin = None
     if product_table:
         cos, sin = gkv.rope_table(case.cos.shape[0])
@@ -26,14 +26,19 @@ def run_gpu(case: DecodeCase, gkv, torch, device, split_tokens=0, out_dtype=None
     q_out = None
     if not rotate_in_attention:
         q_out = torch.empty(case.B, case.Hq * 64, dtype=torch.float32, device=device)
-    gkv.kv_append(dev["qkv"], case.Hq, dev["cos"], dev["sin"], dev["pos"], view,
-                  seq_lens=dev["seq_lens"], q_out=q_out, dev_err=dev["err"])
+    if not layer_call:
+        gkv.kv_append(dev["qkv"], case.Hq, dev["cos"], dev["sin"], dev["pos"], view,
+                      seq_lens=dev["seq_lens"], q_out=q_out, dev_err=dev["err"])
     max_len = int(case.seq_lens.max())
     ws_bytes = gkv.workspace_bytes(case.B, case.Hkv, max_len, case.window, split_tokens)
     ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device=device)
     out = torch.full((case.B, case.Hq * 64), float("nan"),
                      dtype=out_dtype or torch.float32, device=device)
-    if rotate_in_attention:
+    if layer_call:
+        gkv.decode_layer(dev["qkv"], dev["seq_lens"], max_len, view, dev["sinks"], out,
+                         dev["cos"], dev["sin"], window=case.window, split_tokens=split_tokens,
+                         workspace=ws, dev_err=dev["err"])
+    elif rotate_in_attention:
         gkv.decode_attention(dev["qkv"], dev["seq_lens"], max_len, view, dev["sinks"], out,
                              window=case.window, cos_tab=dev["cos"], sin_tab=dev["sin"],
                              split_tokens=split_tokens, workspace=ws, dev_err=dev["err"])
@@ -112,6 +117,22 @@ def test_config3_window_layer_reduced_batch(gkv, cuda, torch_mod):
     L[:4] = [0, 126, 127, 128]  # partial, exactly full, and wrapped rings
     case = DecodeCase(B, 64, 8, L, window=128, scale=0.5, seed=33)
     check_case(case, run_gpu(case, gkv, torch_mod, cuda))
+
+
+@pytest.mark.parametrize("window", [0, 128])
+def test_decode_layer_call_matches_two_calls(gkv, cuda, torch_mod, window):
+    """gkv_decode_layer (append fused into the prepare launch) writes the same
+    cache bytes as gkv_kv_append and the same output bits as
+    gkv_decode_attention, and both match the oracle."""
+    rng = np.random.default_rng(60 + window)
+    B = 40
+    L = lens_uniform(rng, B, 0, 3000)
+    L[:3] = [0, 127, 128]
+    case = DecodeCase(B, 64, 8, L, window=window, scale=0.5, seed=61 + window)
+    fused = run_gpu(case, gkv, torch_mod, cuda, layer_call=True)
+    check_case(case, fused)
+    two = run_gpu(case, gkv, torch_mod, cuda)
+    assert np.array_equal(fused["out"].view(np.uint32), two["out"].view(np.uint32))
 
 
 # ---- edges ---------------------------------------------------------------------
