@@ -54,7 +54,7 @@ struct PrefillArgs {
 };
 
 template <int NW>
-__global__ __launch_bounds__(NW * 64) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8 ? 4 : 1))) void prefill_kernel(PrefillArgs a) {
   constexpr int D = kHeadDim;
   constexpr int NT = NW * 64;
   constexpr int kLoads = kKTile * (D / 8) / NT; // 16-byte pieces of K (and of V) per thread per tile
