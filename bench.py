@@ -479,7 +479,7 @@ def main() -> int:
             "workload": f"config {args.config}: {cfg['name']}",
             "B": B, "H_q": Hq, "H_kv": Hkv, "head_dim": D, "layers": n_layers,
             "context": f"U[{cfg['lo']},{cfg['hi']}]", "window": cfg["window"],
-            "kv_bytes_per_step": kv_bytes, "split_tokens": args.split_tokens or 512,
+            "kv_bytes_per_step": kv_bytes, "split_tokens": args.split_tokens or "balanced",
             "pool_bytes": pool.device_bytes(),
             "kernel_ms": dict(zip(stages, (round(float(x), 4) for x in stage_ms))),
             "parallelism": "1 GPU",
