@@ -144,3 +144,23 @@ def test_engine_shim_header_compiles(tmp_path):
                         "-I", os.path.join(root, "include"), str(src)],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_pool_calls_reject_null_and_bad_config(gkv):
+    """Host-side argument checks of the pool (no device memory is touched)."""
+    lib = gkv.lib()
+    n = ctypes.c_int32()
+    assert lib.gkv_pool_seq_alloc(None, ctypes.byref(n)) == gkv.GKV_ERR_ARG
+    assert lib.gkv_pool_seq_reserve(None, 0, 10) == gkv.GKV_ERR_ARG
+    assert lib.gkv_pool_seq_free(None, 0) == gkv.GKV_ERR_ARG
+    assert lib.gkv_pool_sync(None, None) == gkv.GKV_ERR_ARG
+    assert lib.gkv_pool_destroy(None) == gkv.GKV_ERR_ARG
+    assert lib.gkv_pool_free_blocks(None) == -1
+    assert lib.gkv_pool_num_blocks(None) == -1
+    h = ctypes.c_void_p()
+    for bad in (dict(n_layers=0), dict(head_dim=128), dict(window=20), dict(max_seqs=0)):
+        cfg = dict(n_layers=2, n_kv_heads=8, head_dim=64, window=128, max_seqs=4,
+                   max_seq_len=256, num_blocks=8, bytes_budget=0, shuffle_seed=0)
+        cfg.update(bad)
+        st = lib.gkv_pool_create(ctypes.byref(gkv.PoolConfig(*cfg.values())), ctypes.byref(h))
+        assert st in (gkv.GKV_ERR_ARG, gkv.GKV_ERR_UNSUPPORTED), (bad, st)
