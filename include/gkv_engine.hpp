@@ -80,6 +80,19 @@ inline void attention_bf16_chunk64(stream_t s, const float *qkv, int row_stride,
         "attention_bf16_chunk64");
 }
 
+// rope_kv_bf16(rotate_q = false) followed by attention_bf16_chunk64, the pair
+// at gpu_engine.hpp:495-498, as one gkv_decode_layer call (the append runs in
+// the attention's first launch). Row b is the new token at row_pos[b].
+inline void rope_kv_attention_bf16(stream_t s, int B, const float *qkv, int row_stride,
+                                   const PagedLayer &layer, int n_q_heads, bf16_t *out,
+                                   int out_stride, const PagedBatch &bt) {
+  check(gkv_decode_layer(s, B, n_q_heads, qkv, row_stride, bt.cos_tab, bt.sin_tab,
+                         bt.seq_lens, bt.max_seq_len, layer.view, layer.window, layer.sinks, 0,
+                         bt.workspace, bt.workspace_bytes, out, out_stride, GKV_BF16,
+                         bt.dev_err),
+        "rope_kv_attention_bf16");
+}
+
 // The exact path's fp32-output attention (attention_exact,
 // getp-csrc/kernels/attention.hpp:18-83), same arguments, fp32 [B][out_stride].
 inline void attention_exact(stream_t s, const float *qkv, int row_stride,
