@@ -5,7 +5,8 @@
 // tables, then per layer rope_kv_bf16(rotate_q = false) and
 // attention_bf16_chunk64 with the query rotated on load.
 //
-//   gkv_engine_demo <in.bin> <out.bin>
+//   gkv_engine_demo <in.bin> <out.bin> [fused]
+// fused: the one-call form rope_kv_attention_bf16 instead of the two calls.
 // in.bin:  int32 P, B, Hq, Hkv, n_layers, window; fp32 qkv [P][n_layers][B][(Hq+2Hkv)*64];
 //          fp32 sinks [n_layers][Hq]
 // out.bin: bf16 [P][n_layers][B][Hq*64] attention outputs of every step
@@ -28,10 +29,11 @@
   } while (0)
 
 int main(int argc, char **argv) {
-  if (argc != 3) {
-    fprintf(stderr, "usage: %s in.bin out.bin\n", argv[0]);
+  if (argc != 3 && argc != 4) {
+    fprintf(stderr, "usage: %s in.bin out.bin [fused]\n", argv[0]);
     return 2;
   }
+  const bool fused = argc == 4;
   FILE *f = fopen(argv[1], "rb");
   if (!f)
     return 2;
@@ -110,8 +112,12 @@ int main(int argc, char **argv) {
     for (int l = 0; l < NL; l++) {
       HIP_OK(hipMemcpyAsync(d_qkv, qkv.data() + ((size_t)p * NL + l) * B * QKV,
                             (size_t)B * QKV * 4, hipMemcpyHostToDevice, s));
-      gkv_engine::rope_kv_bf16(s, B, d_qkv, QKV, bt, Hq, layers[l], /*rotate_q=*/false);
-      gkv_engine::attention_bf16_chunk64(s, d_qkv, QKV, layers[l], Hq, d_out, ATT, B, bt);
+      if (fused) {
+        gkv_engine::rope_kv_attention_bf16(s, B, d_qkv, QKV, layers[l], Hq, d_out, ATT, bt);
+      } else {
+        gkv_engine::rope_kv_bf16(s, B, d_qkv, QKV, bt, Hq, layers[l], /*rotate_q=*/false);
+        gkv_engine::attention_bf16_chunk64(s, d_qkv, QKV, layers[l], Hq, d_out, ATT, B, bt);
+      }
       HIP_OK(hipMemcpyAsync(out.data() + ((size_t)p * NL + l) * B * ATT, d_out,
                             (size_t)B * ATT * 2, hipMemcpyDeviceToHost, s));
       HIP_OK(hipStreamSynchronize(s));

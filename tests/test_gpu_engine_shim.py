@@ -19,7 +19,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 DEMO = os.path.join(ROOT, "optimize_inference_gpt-oss_amd", "gkv_engine_demo")
 
 
-def test_engine_shim_decode_loop(oracle, cuda, tmp_path):
+@pytest.mark.parametrize("fused", [False, True])
+def test_engine_shim_decode_loop(oracle, cuda, tmp_path, fused):
     if not os.path.exists(DEMO):
         pytest.fail("gkv_engine_demo is not built (run __graft_entry__.build())")
     P, B, Hq, Hkv, NL, W = 40, 3, 64, 8, 2, 32
@@ -31,7 +32,8 @@ def test_engine_shim_decode_loop(oracle, cuda, tmp_path):
         np.array([P, B, Hq, Hkv, NL, W], np.int32).tofile(f)
         qkv.tofile(f)
         sinks.tofile(f)
-    r = subprocess.run([DEMO, str(inp), str(outp)], capture_output=True, text=True, timeout=90)
+    cmd = [DEMO, str(inp), str(outp)] + (["fused"] if fused else [])
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=90)
     assert r.returncode == 0, r.stderr
     got = np.fromfile(outp, np.uint16).reshape(P, NL, B, Hq, 64)
     got = oracle.from_bf16(got)
