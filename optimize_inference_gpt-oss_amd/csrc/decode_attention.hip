@@ -636,7 +636,7 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
 
 // ---- host side --------------------------------------------------------------------
 
-constexpr int kRing = 5;
+constexpr int kRing = 4;
 
 // Ring depth of the split kernel (default kRing; the tuning variable
 // GKV_DECODE_RING = 3..8 picks another, read once).
@@ -658,8 +658,8 @@ static const void *split_kernel_fn(int ring) {
   switch (ring) {
   case 3:
     return (const void *)decode_split_kernel<3>;
-  case 4:
-    return (const void *)decode_split_kernel<4>;
+  case 5:
+    return (const void *)decode_split_kernel<5>;
   case 6:
     return (const void *)decode_split_kernel<6>;
   case 7:
@@ -667,7 +667,7 @@ static const void *split_kernel_fn(int ring) {
   case 8:
     return (const void *)decode_split_kernel<8>;
   default:
-    return (const void *)decode_split_kernel<5>;
+    return (const void *)decode_split_kernel<4>;
   }
 }
 
@@ -830,8 +830,8 @@ static int launch_split(const DecodeArgs &a, hipStream_t s) {
   case 3:
     launch_split_ring<3>(a, grid, block, s);
     break;
-  case 4:
-    launch_split_ring<4>(a, grid, block, s);
+  case 5:
+    launch_split_ring<5>(a, grid, block, s);
     break;
   case 6:
     launch_split_ring<6>(a, grid, block, s);
@@ -843,7 +843,7 @@ static int launch_split(const DecodeArgs &a, hipStream_t s) {
     launch_split_ring<8>(a, grid, block, s);
     break;
   default:
-    launch_split_ring<5>(a, grid, block, s);
+    launch_split_ring<4>(a, grid, block, s);
   }
   return launch_status("decode_split_kernel");
 }
