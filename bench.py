@@ -78,15 +78,26 @@ class Layer:
 
 
 def fill_cache(torch, gkv, pool, n_layers, dev, seed):
-    """Random bf16 N(0,1)*0.5 in every cache array of the pool (the history)."""
+    """Random history in every cache array of the pool: bf16 N(0,1)*0.5 for K
+    (and V); for an int8 V cache, random codes in [-127, 127] and scales of
+    N(0,1)*0.5 data (max |v| / 127 of 64 values, about 0.012)."""
     for layer in range(n_layers):
         v = pool.view(layer)
-        for i, base in enumerate((v.k, v.v)):
-            n = v.num_blocks * v.n_kv_heads * 16 * D
+        n = v.num_blocks * v.n_kv_heads * 16 * D
+        bases = [(v.k, "bf16"), (v.v, "int8" if v.v_format == gkv.V_INT8 else "bf16")]
+        if v.v_format == gkv.V_INT8:
+            bases.append((v.v_scale, "scale"))
+        for i, (base, kind) in enumerate(bases):
             g = torch.Generator(device=dev)
-            g.manual_seed(seed * 1000 + 2 * layer + i)
-            t = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.5, generator=g)
-            gkv.hip_memcpy_d2d(base, t.data_ptr(), n * 2)
+            g.manual_seed(seed * 1000 + 3 * layer + i)
+            if kind == "bf16":
+                t = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.5, generator=g)
+            elif kind == "int8":
+                t = torch.randint(-127, 128, (n,), generator=g, device=dev, dtype=torch.int8)
+            else:
+                t = torch.empty(n // D, dtype=torch.float32, device=dev).uniform_(
+                    0.009, 0.015, generator=g)
+            gkv.hip_memcpy_d2d(base, t.data_ptr(), t.numel() * t.element_size())
             torch.cuda.synchronize()
             del t
 
@@ -105,7 +116,24 @@ def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, th
     n_blk_total = v.num_blocks
     # gather the sampled sequences' logical caches to the host
     k_arr = gkv_cache_tensor(torch, v.k, n_blk_total, Hkv, (16, D))
-    v_arr = gkv_cache_tensor(torch, v.v, n_blk_total, Hkv, (D, 16))
+    v_int8 = v.v_format == gkv.V_INT8
+    if v_int8:
+        # int8 codes and scales, dequantized to fp32 [block, head, dim, token]
+        n = n_blk_total * Hkv * 16 * D
+        codes = torch.empty(n, dtype=torch.int8, device="cuda")
+        gkv.hip_memcpy_d2d(codes.data_ptr(), v.v, n)
+        scl = torch.empty(n // D, dtype=torch.float32, device="cuda")
+        gkv.hip_memcpy_d2d(scl.data_ptr(), v.v_scale, n // D * 4)
+        torch.cuda.synchronize()
+        d = torch.arange(D, device="cuda")
+        t16 = torch.arange(16, device="cuda")
+        off = ((d[:, None] % 16) * 4 + t16[None, :] // 4) * 16 + (d[:, None] // 16) * 4 \
+            + t16[None, :] % 4                                   # [dim, token]
+        codes = codes.view(n_blk_total, Hkv, 16 * D)[:, :, off.reshape(-1)]
+        v_arr = (codes.float().view(n_blk_total, Hkv, D, 16)
+                 * scl.view(n_blk_total, Hkv, 1, 16))
+    else:
+        v_arr = gkv_cache_tensor(torch, v.v, n_blk_total, Hkv, (D, 16))
     table = table_tensor(torch, v, sample_seqs)
     seq_lens = (L[:sample_seqs] + 1).astype(np.int32)
     W = layer_state.window
@@ -135,7 +163,7 @@ def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, th
             break
     dt /= reps
     n_read = np.minimum(seq_lens, W) if W else seq_lens
-    nbytes = float(n_read.sum()) * Hkv * D * 2 * 2
+    nbytes = float(n_read.sum()) * Hkv * (D * 2 + (D + 4 if v_int8 else D * 2))
     got = gpu_out[:sample_seqs].float().cpu().numpy().reshape(sample_seqs, Hq, D)
     err = np.abs(got - ref)
     ok = bool(np.all(err <= 2e-3 + 1e-2 * np.abs(ref)))
@@ -319,6 +347,9 @@ def main() -> int:
     ap.add_argument("--lengths", default="random", choices=["random", "sorted", "fixed"],
                     help="diagnostics: context lengths in batch order as drawn, sorted "
                          "longest first, or all equal to the mean")
+    ap.add_argument("--v-int8", action="store_true",
+                    help="the reference's int8-V cache (codes + fp32 scale per token and "
+                         "head) instead of bf16 V")
     ap.add_argument("--separate-append", action="store_true",
                     help="append with gkv_kv_append, then gkv_decode_attention (four launches "
                          "per layer instead of gkv_decode_layer's three)")
@@ -356,7 +387,8 @@ def main() -> int:
     need = int(((seq_lens + 15) // 16).sum())
     pool = gkv.Pool(n_layers=n_layers, n_kv_heads=Hkv, max_seqs=B, max_seq_len=max_len,
                     window=cfg["window"], num_blocks=need + 64,
-                    shuffle_seed=0 if args.sequential_blocks else args.seed)
+                    shuffle_seed=0 if args.sequential_blocks else args.seed,
+                    v_format=gkv.V_INT8 if args.v_int8 else gkv.V_BF16)
     seqs = [pool.seq_alloc() for _ in range(B)]
     assert seqs == list(range(B))  # row b of the batch is sequence id b
     for b in range(B):
@@ -377,9 +409,13 @@ def main() -> int:
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
 
+    # algorithmic bytes per cached token and kv head: K bf16 (128 B) + V bf16
+    # (128 B), or int8 V (64 B of codes + a 4-byte scale)
+    per_token = D * 2 + (D + 4 if args.v_int8 else D * 2)
+
     def bytes_of(layer: Layer) -> float:
         n = np.minimum(seq_lens, layer.window) if layer.window else seq_lens
-        return float(n.sum()) * Hkv * D * 2 * 2
+        return float(n.sum()) * Hkv * per_token
 
     kv_bytes = sum(bytes_of(l) for l in layers)
 
@@ -479,7 +515,7 @@ def main() -> int:
             "workload": f"config {args.config}: {cfg['name']}",
             "B": B, "H_q": Hq, "H_kv": Hkv, "head_dim": D, "layers": n_layers,
             "context": f"U[{cfg['lo']},{cfg['hi']}]", "window": cfg["window"],
-            "kv_bytes_per_step": kv_bytes, "split_tokens": args.split_tokens or "balanced",
+            "kv_bytes_per_step": kv_bytes, "v_cache": "int8+scale" if args.v_int8 else "bf16", "split_tokens": args.split_tokens or "balanced",
             "pool_bytes": pool.device_bytes(),
             "kernel_ms": dict(zip(stages, (round(float(x), 4) for x in stage_ms))),
             "parallelism": "1 GPU",

@@ -61,15 +61,25 @@ typedef enum {
 
 typedef enum { GKV_F32 = 0, GKV_BF16 = 1 } gkv_dtype;
 
+/* Storage of the V cache. GKV_V_INT8 is the reference's int8-V cache
+ * (getp-csrc/kernels/fast_misc.hpp:74-84): per token and head, 64 int8 codes
+ * and one fp32 scale = max|v| / 127, code = rint(v * 127 / max|v|). */
+typedef enum { GKV_V_BF16 = 0, GKV_V_INT8 = 1 } gkv_v_format;
+
 /* A paged cache of one layer as the kernels see it. */
 typedef struct {
   void *k;                     /* bf16 [num_blocks][n_kv_heads][16][64] */
-  void *v;                     /* bf16 [num_blocks][n_kv_heads][64][16] */
+  void *v;                     /* GKV_V_BF16: bf16 [num_blocks][n_kv_heads][64][16];
+                                  GKV_V_INT8: int8 [num_blocks][n_kv_heads][1024], code of
+                                  dim d, token t at ((d % 16) * 4 + t / 4) * 16 + (d / 16) * 4
+                                  + t % 4 */
   const int32_t *block_table;  /* int32 [B][table_stride] (device) */
   int32_t table_stride;        /* entries per table row */
   int32_t num_blocks;          /* physical blocks in k / v (ids are checked against it) */
   int32_t n_kv_heads;
   int32_t ring;                /* 0: slot = position; W > 0: slot = position % W */
+  void *v_scale;               /* GKV_V_INT8: fp32 [num_blocks][n_kv_heads][16]; else NULL */
+  int32_t v_format;            /* gkv_v_format (0: bf16) */
 } gkv_cache_view;
 
 const char *gkv_status_string(int status);
@@ -222,6 +232,7 @@ typedef struct {
                               0: 90% of hipMemGetInfo's free memory */
   uint64_t shuffle_seed;   /* 0: blocks handed out in id order; else a seeded
                               permutation (scattered physical placement) */
+  int32_t v_format;        /* gkv_v_format of every layer's V cache (0: bf16) */
 } gkv_pool_config;
 
 int gkv_pool_create(const gkv_pool_config *cfg, gkv_pool **out);

@@ -98,6 +98,7 @@ struct DecodeArgs {
   const float *cos_tab, *sin_tab;
   const int32_t *seq_lens;
   const uint16_t *kc, *vc;
+  const float *vs;    // int8 V: fp32 scales [block][head][16]
   const int32_t *table;
   int table_stride, num_blocks, n_kv_heads, window;
   int max_len;        // host bound of the tokens attended per sequence
@@ -147,6 +148,17 @@ __device__ __forceinline__ bf16x8 pack_pieces(const float (&x)[8], bool lo) {
     r[i] = lo ? (__bf16)(x[i] - (float)hi) : hi;
   }
   return r;
+}
+
+// Four int8 codes (one per byte) -> four bf16 (exact: |code| <= 127), in order.
+__device__ __forceinline__ u32x2 int8x4_to_bf16x4(uint32_t w) {
+  uint32_t h[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int c = (int)(w << (24 - 8 * i)) >> 24; // sign-extended byte i
+    h[i] = __float_as_uint((float)c) >> 16;
+  }
+  return u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
 }
 
 // ---- prep -----------------------------------------------------------------------
@@ -316,7 +328,7 @@ __global__ __launch_bounds__(kPrepThreads) void decode_layer_prep_kernel(DecodeA
 
 // R: depth of the register ring of loaded steps (R - 1 steps in flight ahead
 // of the one being computed).
-template <int R>
+template <int R, bool VQ>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(kSplitWaves / 4)))
 void decode_split_kernel(DecodeArgs a) {
   constexpr int D = kHeadDim;
@@ -340,6 +352,7 @@ void decode_split_kernel(DecodeArgs a) {
   const uint32_t k_off = (uint32_t)(col * D + 8 * kg) * 2;
   const uint32_t v_off = (uint32_t)(col * kBlockTokens + 4 * kg) * 2; // + nn * 512
   const size_t head_bytes = (size_t)kBlockTokens * D * 2;               // 2 KB
+  const uint32_t vq_off = (uint32_t)(col * 4 + kg) * 16;                 // int8 V piece
 
   // Block ids and step records of the range, one per lane per register.
   const int e0 = rs / kBlockTokens, s0 = rs / kStep;
@@ -399,11 +412,26 @@ void decode_split_kernel(DecodeArgs a) {
     kr[1] = __builtin_amdgcn_raw_buffer_load_b128(k0, k_off + 64, 0, 0);
     kr[2] = __builtin_amdgcn_raw_buffer_load_b128(k1, k_off, 0, 0);
     kr[3] = __builtin_amdgcn_raw_buffer_load_b128(k1, k_off + 64, 0, 0);
+    if (VQ) {
+      // int8 V: one 16-byte piece per block (dims col + 16nn, tokens
+      // 4kg..4kg+3), then the 4 scales of those tokens per block
+      const size_t q0 = ((size_t)p0 * a.n_kv_heads + g) * (head_bytes / 2);
+      const size_t q1 = ((size_t)p1 * a.n_kv_heads + g) * (head_bytes / 2);
+      const __amdgpu_buffer_rsrc_t c0 = head_rsrc((const char *)a.vc + q0);
+      const __amdgpu_buffer_rsrc_t c1 = head_rsrc((const char *)a.vc + q1);
+      const __amdgpu_buffer_rsrc_t s0 = head_rsrc((const char *)a.vs + q0 / 16);
+      const __amdgpu_buffer_rsrc_t s1 = head_rsrc((const char *)a.vs + q1 / 16);
+      vr[0] = __builtin_amdgcn_raw_buffer_load_b128(c0, vq_off, 0, 0);
+      vr[1] = __builtin_amdgcn_raw_buffer_load_b128(c1, vq_off, 0, 0);
+      vr[2] = __builtin_amdgcn_raw_buffer_load_b128(s0, 16 * kg, 0, 0);
+      vr[3] = __builtin_amdgcn_raw_buffer_load_b128(s1, 16 * kg, 0, 0);
+    } else {
 #pragma unroll
-    for (int nn = 0; nn < 4; nn++) {
-      const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(v0, v_off + nn * 512, 0, 0);
-      const u32x2 y = __builtin_amdgcn_raw_buffer_load_b64(v1, v_off + nn * 512, 0, 0);
-      vr[nn] = u32x4{x[0], x[1], y[0], y[1]};
+      for (int nn = 0; nn < 4; nn++) {
+        const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(v0, v_off + nn * 512, 0, 0);
+        const u32x2 y = __builtin_amdgcn_raw_buffer_load_b64(v1, v_off + nn * 512, 0, 0);
+        vr[nn] = u32x4{x[0], x[1], y[0], y[1]};
+      }
     }
     if (!kQAtSegmentStart || (rc & 0x80) || step == 0) {
       const u32x4 *qs = a.qops + (((int64_t)(rc >> 8) * a.n_kv_heads + g) * 64 + lane) * 2;
@@ -529,7 +557,7 @@ void decode_split_kernel(DecodeArgs a) {
           if (16 * jt + 4 * kg + r >= valid || blk_bad)
             sc[4 * jt + r] = -INFINITY;
 #pragma unroll
-        for (int h2 = 0; h2 < 2; h2++) {
+        for (int h2 = 0; h2 < 2 && !VQ; h2++) {
           const int tk = 16 * jt + 4 * kg + 2 * h2;
           const uint32_t keep = blk_bad ? 0u
                                         : ((tk < valid ? 0x0000ffffu : 0u) |
@@ -565,11 +593,28 @@ void decode_split_kernel(DecodeArgs a) {
       p[i] = __builtin_amdgcn_exp2f(sc[i] - m_run);
       lsum += p[i];
     }
-    const bf16x8 pop = pack_pieces(p, lo);
+    if (VQ) {
+      // int8 V: the token's scale goes into its weight (the codes are exact
+      // in bf16); a masked token's weight is 0 whatever its scale holds
 #pragma unroll
-    for (int nn = 0; nn < 4; nn++)
-      o[nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vr[nn]), pop,
-                                                      o[nn], 0, 0, 0);
+      for (int i = 0; i < 8; i++) {
+        const float sc_t = __uint_as_float(vr[2 + (i >> 2)][i & 3]);
+        p[i] = p[i] == 0.0f ? 0.0f : p[i] * sc_t;
+      }
+      const bf16x8 pop = pack_pieces(p, lo);
+#pragma unroll
+      for (int nn = 0; nn < 4; nn++) {
+        const u32x2 x = int8x4_to_bf16x4(vr[0][nn]), y = int8x4_to_bf16x4(vr[1][nn]);
+        const bf16x8 vop = __builtin_bit_cast(bf16x8, u32x4{x[0], x[1], y[0], y[1]});
+        o[nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, o[nn], 0, 0, 0);
+      }
+    } else {
+      const bf16x8 pop = pack_pieces(p, lo);
+#pragma unroll
+      for (int nn = 0; nn < 4; nn++)
+        o[nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vr[nn]), pop,
+                                                        o[nn], 0, 0, 0);
+    }
   };
 
   // Ring: slot r holds virtual step base + r; the load for v + R - 1 goes out
@@ -651,23 +696,26 @@ static int ring_depth() {
 
 template <int R>
 static void launch_split_ring(const DecodeArgs &a, dim3 grid, dim3 block, hipStream_t s) {
-  hipLaunchKernelGGL(decode_split_kernel<R>, grid, block, 0, s, a);
+  if (a.vs)
+    hipLaunchKernelGGL((decode_split_kernel<R, true>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_split_kernel<R, false>), grid, block, 0, s, a);
 }
 
 static const void *split_kernel_fn(int ring) {
   switch (ring) {
   case 3:
-    return (const void *)decode_split_kernel<3>;
+    return (const void *)decode_split_kernel<3, false>;
   case 5:
-    return (const void *)decode_split_kernel<5>;
+    return (const void *)decode_split_kernel<5, false>;
   case 6:
-    return (const void *)decode_split_kernel<6>;
+    return (const void *)decode_split_kernel<6, false>;
   case 7:
-    return (const void *)decode_split_kernel<7>;
+    return (const void *)decode_split_kernel<7, false>;
   case 8:
-    return (const void *)decode_split_kernel<8>;
+    return (const void *)decode_split_kernel<8, false>;
   default:
-    return (const void *)decode_split_kernel<4>;
+    return (const void *)decode_split_kernel<4, false>;
   }
 }
 
@@ -732,6 +780,10 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
     return GKV_ERR_ARG;
   if (n_q_heads % cache.n_kv_heads != 0)
     return GKV_ERR_ARG;
+  if (cache.v_format != GKV_V_BF16 && cache.v_format != GKV_V_INT8)
+    return GKV_ERR_ARG;
+  if (need_cache && cache.v_format == GKV_V_INT8 && !cache.v_scale)
+    return GKV_ERR_ARG;
   if (cache.n_kv_heads > 8 || B > kMaxBatch)
     return GKV_ERR_UNSUPPORTED; // combine: one wave per kv head; prep: prefix sums in LDS
   const int G = n_q_heads / cache.n_kv_heads;
@@ -778,6 +830,7 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
   a.seq_lens = seq_lens;
   a.kc = (const uint16_t *)cache.k;
   a.vc = (const uint16_t *)cache.v;
+  a.vs = cache.v_format == GKV_V_INT8 ? (const float *)cache.v_scale : nullptr;
   a.table = cache.block_table;
   a.table_stride = cache.table_stride;
   a.num_blocks = cache.num_blocks;
@@ -957,6 +1010,8 @@ static int layer_append_args(AppendArgs &ap, int32_t B, int32_t n_q_heads, const
   ap.q_out_stride = 0;
   ap.k_pack = ap.v_pack = nullptr;
   ap.dev_err = dev_err;
+  ap.v_int8 = cache.v_format == GKV_V_INT8;
+  ap.vs = (float *)cache.v_scale;
   (void)B;
   return GKV_OK;
 }

@@ -44,6 +44,10 @@ extern "C" int gkv_kv_append(void *stream, int32_t n_rows, const float *qkv, int
     return GKV_ERR_ARG;
   if (cache.ring % kBlockTokens != 0)
     return GKV_ERR_UNSUPPORTED;
+  if (cache.v_format != GKV_V_BF16 && cache.v_format != GKV_V_INT8)
+    return GKV_ERR_ARG;
+  if (to_cache && cache.v_format == GKV_V_INT8 && !cache.v_scale)
+    return GKV_ERR_ARG;
   if (n_rows == 0)
     return GKV_OK;
   AppendArgs a;
@@ -67,6 +71,8 @@ extern "C" int gkv_kv_append(void *stream, int32_t n_rows, const float *qkv, int
   a.k_pack = (uint16_t *)k_pack;
   a.v_pack = (uint16_t *)v_pack;
   a.dev_err = dev_err;
+  a.v_int8 = cache.v_format == GKV_V_INT8;
+  a.vs = (float *)cache.v_scale;
   hipLaunchKernelGGL(kv_append_kernel, dim3(n_rows), dim3(256), 0, (hipStream_t)stream, a);
   return launch_status(__func__);
 }

@@ -19,7 +19,16 @@ struct AppendArgs {
   int64_t q_out_stride;
   uint16_t *k_pack, *v_pack;
   uint32_t *dev_err;
+  float *vs;   // int8 V: fp32 scales [block][head][16]; nullptr for bf16 V
+  int v_int8;  // 1: V is stored as int8 codes + scales (gkv_v_format GKV_V_INT8)
 };
+
+// Offset of dim d, token t inside one head's 1 KB int8 V block: lane (kg, i)
+// of the attention kernel finds the codes of dims i, i+16, i+32, i+48 for
+// tokens 4kg..4kg+3 in one 16-byte piece.
+__host__ __device__ __forceinline__ int v_int8_offset(int d, int t) {
+  return ((d % 16) * 4 + t / 4) * 16 + (d / 16) * 4 + t % 4;
+}
 
 // Row r of the call, by nt threads numbered tid = 0 .. nt-1.
 __device__ __forceinline__ void append_row(const AppendArgs &a, int r, int tid, int nt) {
@@ -87,6 +96,30 @@ __device__ __forceinline__ void append_row(const AppendArgs &a, int r, int tid, 
       kp[i] = k1;
       kp[HALF + i] = k2;
     }
+  }
+  if (a.v_int8) {
+    // One wave per head (nt and kv_dim are multiples of 64): the head's
+    // max |v| across the wave, then the reference's rule,
+    // getp-csrc/kernels/fast_misc.hpp:74-84.
+    for (int idx = tid; idx < kv_dim; idx += nt) {
+      const int g = idx / D, d = idx % D;
+      const float x = vr[idx];
+      float amax = fabsf(x);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1)
+        amax = fmaxf(amax, __shfl_xor(amax, o));
+      const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+      const float c = fminf(fmaxf(rintf(x * inv), -127.0f), 127.0f);
+      if (store) {
+        int8_t *vq = (int8_t *)a.vc + vbase + (int64_t)g * (kBlockTokens * D);
+        vq[v_int8_offset(d, off)] = (int8_t)c;
+        if (d == 0)
+          a.vs[vbase / D + (int64_t)g * kBlockTokens + off] = amax / 127.0f;
+      }
+      if (a.v_pack)
+        a.v_pack[(int64_t)r * kv_dim + idx] = f32_to_bf16_rne(x);
+    }
+    return;
   }
   for (int idx = tid; idx < kv_dim; idx += nt) {
     const int g = idx / D, d = idx % D;

@@ -43,6 +43,7 @@ struct gkv_pool {
   int ring_blocks = 0;  // W / 16
   int64_t num_blocks = 0, num_ring_blocks = 0;
   std::vector<void *> k_full, v_full, k_ring, v_ring;
+  std::vector<void *> s_full, s_ring; // fp32 V scales (int8 V only)
   int32_t *d_table = nullptr, *d_ring_table = nullptr;
   std::vector<int32_t> h_table, h_ring_table;
   std::vector<int32_t> free_blocks; // stack; back() is handed out next
@@ -52,7 +53,7 @@ struct gkv_pool {
   int64_t device_bytes = 0;
 
   ~gkv_pool() {
-    for (auto *vec : {&k_full, &v_full, &k_ring, &v_ring})
+    for (auto *vec : {&k_full, &v_full, &k_ring, &v_ring, &s_full, &s_ring})
       for (void *p : *vec)
         if (p)
           (void)hipFree(p);
@@ -63,8 +64,16 @@ struct gkv_pool {
   }
 };
 
-static int64_t block_bytes_per_layer(int n_kv_heads) {
-  return (int64_t)2 * n_kv_heads * kBT * kD * 2; // K + V, bf16
+// Bytes of one 16-token block of one layer: K bf16, V bf16 or int8 + fp32 scales.
+static int64_t k_bytes(int n_kv_heads) { return (int64_t)n_kv_heads * kBT * kD * 2; }
+static int64_t v_bytes(int n_kv_heads, int v_format) {
+  return v_format == GKV_V_INT8 ? (int64_t)n_kv_heads * kBT * kD : k_bytes(n_kv_heads);
+}
+static int64_t s_bytes(int n_kv_heads, int v_format) {
+  return v_format == GKV_V_INT8 ? (int64_t)n_kv_heads * kBT * 4 : 0;
+}
+static int64_t block_bytes_per_layer(int n_kv_heads, int v_format) {
+  return k_bytes(n_kv_heads) + v_bytes(n_kv_heads, v_format) + s_bytes(n_kv_heads, v_format);
 }
 
 extern "C" int gkv_pool_create(const gkv_pool_config *cfg, gkv_pool **out) {
@@ -77,6 +86,8 @@ extern "C" int gkv_pool_create(const gkv_pool_config *cfg, gkv_pool **out) {
     return GKV_ERR_ARG;
   if (c.head_dim != kD || c.window % kBT != 0)
     return GKV_ERR_UNSUPPORTED;
+  if (c.v_format != GKV_V_BF16 && c.v_format != GKV_V_INT8)
+    return GKV_ERR_ARG;
   gkv_pool *p = new (std::nothrow) gkv_pool();
   if (!p)
     return GKV_ERR_CAPACITY;
@@ -91,7 +102,7 @@ extern "C" int gkv_pool_create(const gkv_pool_config *cfg, gkv_pool **out) {
   p->table_stride = (c.max_seq_len + kBT - 1) / kBT;
   p->ring_blocks = c.window / kBT;
   p->num_ring_blocks = (int64_t)c.max_seqs * p->ring_blocks;
-  const int64_t bpl = block_bytes_per_layer(c.n_kv_heads);
+  const int64_t bpl = block_bytes_per_layer(c.n_kv_heads, c.v_format);
   const int64_t ring_bytes = p->num_ring_blocks * bpl * p->n_window;
   const int64_t table_bytes =
       ((int64_t)c.max_seqs * p->table_stride + (int64_t)c.max_seqs * p->ring_blocks) * 4;
@@ -132,18 +143,23 @@ extern "C" int gkv_pool_create(const gkv_pool_config *cfg, gkv_pool **out) {
     p->device_bytes += bytes;
     return true;
   };
-  const int64_t half_block = bpl / 2;
+  const int64_t kb = k_bytes(c.n_kv_heads), vb = v_bytes(c.n_kv_heads, c.v_format);
+  const int64_t sb = s_bytes(c.n_kv_heads, c.v_format);
   bool ok = true;
   p->k_full.assign(p->n_full, nullptr);
   p->v_full.assign(p->n_full, nullptr);
+  p->s_full.assign(p->n_full, nullptr);
   p->k_ring.assign(p->n_window, nullptr);
   p->v_ring.assign(p->n_window, nullptr);
+  p->s_ring.assign(p->n_window, nullptr);
   for (int i = 0; ok && i < p->n_full; i++)
-    ok = dev_alloc(&p->k_full[i], p->num_blocks * half_block) &&
-         dev_alloc(&p->v_full[i], p->num_blocks * half_block);
+    ok = dev_alloc(&p->k_full[i], p->num_blocks * kb) &&
+         dev_alloc(&p->v_full[i], p->num_blocks * vb) &&
+         dev_alloc(&p->s_full[i], p->num_blocks * sb);
   for (int i = 0; ok && i < p->n_window; i++)
-    ok = dev_alloc(&p->k_ring[i], p->num_ring_blocks * half_block) &&
-         dev_alloc(&p->v_ring[i], p->num_ring_blocks * half_block);
+    ok = dev_alloc(&p->k_ring[i], p->num_ring_blocks * kb) &&
+         dev_alloc(&p->v_ring[i], p->num_ring_blocks * vb) &&
+         dev_alloc(&p->s_ring[i], p->num_ring_blocks * sb);
   ok = ok && dev_alloc((void **)&p->d_table, (int64_t)c.max_seqs * p->table_stride * 4);
   if (ok && p->ring_blocks > 0)
     ok = dev_alloc((void **)&p->d_ring_table, (int64_t)c.max_seqs * p->ring_blocks * 4);
@@ -266,9 +282,11 @@ extern "C" int gkv_pool_layer_view_from(const gkv_pool *pool, int32_t layer, int
   const int i = pool->layer_index[layer];
   gkv_cache_view v{};
   v.n_kv_heads = pool->cfg.n_kv_heads;
+  v.v_format = pool->cfg.v_format;
   if (pool->layer_is_window[layer]) {
     v.k = pool->k_ring[i];
     v.v = pool->v_ring[i];
+    v.v_scale = pool->s_ring[i];
     v.block_table = pool->d_ring_table + (size_t)first_seq * pool->ring_blocks;
     v.table_stride = pool->ring_blocks;
     v.num_blocks = (int32_t)pool->num_ring_blocks;
@@ -276,6 +294,7 @@ extern "C" int gkv_pool_layer_view_from(const gkv_pool *pool, int32_t layer, int
   } else {
     v.k = pool->k_full[i];
     v.v = pool->v_full[i];
+    v.v_scale = pool->s_full[i];
     v.block_table = pool->d_table + (size_t)first_seq * pool->table_stride;
     v.table_stride = pool->table_stride;
     v.num_blocks = (int32_t)pool->num_blocks;

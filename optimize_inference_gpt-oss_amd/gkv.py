@@ -35,7 +35,11 @@ _sz = ctypes.c_size_t
 
 class CacheView(ctypes.Structure):
     _fields_ = [("k", _vp), ("v", _vp), ("block_table", _vp), ("table_stride", _i32),
-                ("num_blocks", _i32), ("n_kv_heads", _i32), ("ring", _i32)]
+                ("num_blocks", _i32), ("n_kv_heads", _i32), ("ring", _i32),
+                ("v_scale", _vp), ("v_format", _i32)]
+
+
+V_BF16, V_INT8 = 0, 1
 
 
 class RopeConfig(ctypes.Structure):
@@ -46,7 +50,7 @@ class RopeConfig(ctypes.Structure):
 class PoolConfig(ctypes.Structure):
     _fields_ = [("n_layers", _i32), ("n_kv_heads", _i32), ("head_dim", _i32), ("window", _i32),
                 ("max_seqs", _i32), ("max_seq_len", _i32), ("num_blocks", _i64),
-                ("bytes_budget", _i64), ("shuffle_seed", _u64)]
+                ("bytes_budget", _i64), ("shuffle_seed", _u64), ("v_format", _i32)]
 
 
 GPT_OSS_ROPE = dict(base=150000.0, head_dim=64, scaling_factor=32.0,
@@ -183,11 +187,13 @@ def rope_table(n_pos: int, **overrides):
     return c, s
 
 
-def cache_view(k, v, block_table, n_kv_heads: int, ring: int = 0) -> CacheView:
+def cache_view(k, v, block_table, n_kv_heads: int, ring: int = 0, v_scale=None) -> CacheView:
     """View over torch tensors k [NB, Hkv, 16, 64], v [NB, Hkv, 64, 16] (bf16 or int16),
-    block_table int32 [B, stride]."""
+    block_table int32 [B, stride]. With v_scale (fp32 [NB, Hkv, 16]) the V cache is
+    int8 codes [NB, Hkv, 1024] (GKV_V_INT8)."""
     return CacheView(ptr(k), ptr(v), ptr(block_table), int(block_table.shape[1]),
-                     int(k.shape[0]), int(n_kv_heads), int(ring))
+                     int(k.shape[0]), int(n_kv_heads), int(ring), ptr(v_scale),
+                     V_INT8 if v_scale is not None else V_BF16)
 
 
 def kv_append(qkv, n_q_heads, cos_tab, sin_tab, row_pos, view: CacheView, row_seq=None,
@@ -251,9 +257,9 @@ class Pool:
     """Paged KV pool (gkv_pool_*)."""
 
     def __init__(self, n_layers, n_kv_heads, max_seqs, max_seq_len, window=128, num_blocks=0,
-                 bytes_budget=0, shuffle_seed=0, head_dim=64):
+                 bytes_budget=0, shuffle_seed=0, head_dim=64, v_format=0):
         self.cfg = PoolConfig(n_layers, n_kv_heads, head_dim, window, max_seqs, max_seq_len,
-                              num_blocks, bytes_budget, shuffle_seed)
+                              num_blocks, bytes_budget, shuffle_seed, v_format)
         h = _vp()
         check("gkv_pool_create", lib().gkv_pool_create(ctypes.byref(self.cfg), ctypes.byref(h)))
         self.h = h

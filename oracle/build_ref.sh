@@ -20,3 +20,12 @@ hipcc --std=c++17 -O3 -fopenmp -march=x86-64-v3 -DTESTING -fPIC -shared \
   "$HERE/ref_harness.cpp" "$REF/tokenizer.cpp" -o "$HERE/_ref/libref.so.tmp"
 mv "$HERE/_ref/libref.so.tmp" "$HERE/_ref/libref.so"
 echo "build_ref: wrote $HERE/_ref/libref.so"
+# The int8-V rule lives in the reference's attention test (host code); its
+# file is compiled where it lies, around oracle/ref_q8_harness.cpp.
+if [ -f "$REF/getp-csrc/tests/attn_test.cpp" ]; then
+  hipcc --std=c++17 -O3 -fPIC -shared --offload-arch=gfx950 -w -I"$REF/getp-csrc" \
+    "$HERE/ref_q8_harness.cpp" -o "$HERE/_ref/libref_q8.so.tmp"
+  mv "$HERE/_ref/libref_q8.so.tmp" "$HERE/_ref/libref_q8.so"
+  echo "build_ref: wrote $HERE/_ref/libref_q8.so"
+fi
+

@@ -271,3 +271,22 @@ void orc_kv_append(int B, int n_q_heads, int n_kv_heads, int head_dim, const flo
   }
   free(tmp);
 }
+
+/* fast_misc.hpp:74-84 / attn_test.cpp:218-226: amax over the head, the
+ * reciprocal 127/amax rounded once, each value times it rounded, then rint
+ * (ties to even) and the clamp. */
+void orc_quantize_v(const float *v, int n_heads, int head_dim, int8_t *codes, float *scales) {
+  for (int h = 0; h < n_heads; h++) {
+    const float *x = v + (long)h * head_dim;
+    float amax = 0.0f;
+    for (int i = 0; i < head_dim; i++)
+      amax = fmaxf(amax, fabsf(x[i]));
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    for (int i = 0; i < head_dim; i++) {
+      float c = rintf(x[i] * inv);
+      c = fminf(fmaxf(c, -127.0f), 127.0f);
+      codes[(long)h * head_dim + i] = (int8_t)c;
+    }
+    scales[h] = amax / 127.0f;
+  }
+}

@@ -93,6 +93,14 @@ void orc_kv_append(int B, int n_q_heads, int n_kv_heads, int head_dim, const flo
                    long row_stride, const float *cos_tab, const float *sin_tab, const int *pos,
                    float *q_rot, float *k_rot, uint16_t *k_bf16, uint16_t *v_bf16);
 
+/* int8 V of one token: per head of head_dim values, scale = max|v| / 127 and
+ * code = clamp(rint(v * (127 / max|v|)), -127, 127) (0 codes and scale 0 for
+ * an all-zero head): the rule of the reference's int8-V cache,
+ * getp-csrc/kernels/fast_misc.hpp:74-84, restated on the host in
+ * getp-csrc/tests/attn_test.cpp:218-226 (quantize_v).
+ *   v[h*head_dim + i] fp32 -> codes[h*head_dim + i], scales[h] */
+void orc_quantize_v(const float *v, int n_heads, int head_dim, int8_t *codes, float *scales);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,6 +60,7 @@ def lib():
         L.orc_prefill_attention.argtypes = [_i, _i, _i, _i, _vp, _vp, _l, _vp, _vp, _l, _vp, _i,
                                             _vp, _l, _i]
         L.orc_prefill_attention.restype = _i
+        L.orc_quantize_v.argtypes = [_vp, _i, _i, _vp, _vp]
         L.orc_kv_append.argtypes = [_i, _i, _i, _i, _vp, _l, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
         _lib = L
     return _lib
@@ -82,6 +83,28 @@ def ref():
         R.ref_decode_one.restype = _i
         _ref = R
     return _ref
+
+
+REF_Q8_PATH = os.path.join(os.path.dirname(REF_PATH), "libref_q8.so")
+_ref_q8 = None
+
+
+def ref_q8_available() -> bool:
+    return os.path.exists(REF_Q8_PATH)
+
+
+def ref_quantize_v(v: np.ndarray):
+    """The reference's own quantize_v (attn_test.cpp:218-226) on one 64-value head."""
+    global _ref_q8
+    if _ref_q8 is None:
+        _ref_q8 = ctypes.CDLL(REF_Q8_PATH)
+        _ref_q8.ref_quantize_v.argtypes = [_vp, _vp, _vp]
+    v = _f32(v)
+    assert v.shape == (64,)
+    codes = np.zeros(64, np.int8)
+    scale = np.zeros(1, np.float32)
+    _ref_q8.ref_quantize_v(_p(v), _p(codes), _p(scale))
+    return codes, float(scale[0])
 
 
 def _p(a: np.ndarray):
@@ -188,6 +211,22 @@ def kv_append(qkv, n_q_heads, n_kv_heads, cos_tab, sin_tab, pos, head_dim=64):
                         _p(kb), _p(vb))
     del kv_dim
     return q_rot, k_rot, kb, vb
+
+
+def quantize_v(v, head_dim=64):
+    """fp32 [..., n_heads, head_dim] -> (int8 codes, same shape; fp32 scales [..., n_heads])."""
+    v = _f32(v)
+    n_heads = v.size // head_dim
+    codes = np.zeros(v.shape, np.int8)
+    scales = np.zeros(v.shape[:-1], np.float32)
+    lib().orc_quantize_v(_p(v), n_heads, head_dim, _p(codes), _p(scales))
+    return codes, scales
+
+
+def dequantize_v(codes, scales):
+    """scale * code in fp32, the values the int8 cache stands for."""
+    return (np.asarray(codes, np.float32) * np.asarray(scales, np.float32)[..., None]).astype(
+        np.float32)
 
 
 # ---- the reference build -------------------------------------------------

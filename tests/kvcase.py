@@ -14,12 +14,20 @@ from oracle import kv_oracle as O
 D = 64
 BT = 16
 BF16_NAN = 0x7FC0
+INT8_POISON = 0x55  # codes of int8-V slots that hold no token
+
+
+def v_int8_offsets(t):
+    """Byte offsets of dims 0..63 of token t (0..15) in a head's 1 KB int8 V block."""
+    d = np.arange(D)
+    return ((d % 16) * 4 + t // 4) * 16 + (d // 16) * 4 + t % 4
 
 
 class DecodeCase:
     def __init__(self, B, n_q_heads, n_kv_heads, ctx_lens, window=0, scale=1.0, seed=0,
-                 extra_blocks=7, rope_rows=None, sink_scale=1.0):
+                 extra_blocks=7, rope_rows=None, sink_scale=1.0, v_int8=False):
         rng = np.random.default_rng(seed)
+        self.v_int8 = v_int8
         self.B, self.Hq, self.Hkv = B, n_q_heads, n_kv_heads
         self.window = window
         self.ring = window
@@ -50,7 +58,12 @@ class DecodeCase:
 
         # Caches, poisoned.
         self.k = np.full((self.num_blocks, n_kv_heads, BT, D), BF16_NAN, np.uint16)
-        self.v = np.full((self.num_blocks, n_kv_heads, D, BT), BF16_NAN, np.uint16)
+        if v_int8:
+            self.v = np.full((self.num_blocks, n_kv_heads, BT * D), INT8_POISON, np.int8)
+            self.vs = np.full((self.num_blocks, n_kv_heads, BT), np.nan, np.float32)
+        else:
+            self.v = np.full((self.num_blocks, n_kv_heads, D, BT), BF16_NAN, np.uint16)
+            self.vs = None
         # Oracle's logical cache (slot-indexed fp32 of the bf16 values).
         S = self.ring if self.ring else int(self.seq_lens.max())
         self.S = S
@@ -67,11 +80,18 @@ class DecodeCase:
             if len(t_hist) == 0:
                 continue
             kh = O.to_bf16(rng.standard_normal((len(t_hist), n_kv_heads, D)) * scale)
-            vh = O.to_bf16(rng.standard_normal((len(t_hist), n_kv_heads, D)) * scale)
+            vf = (rng.standard_normal((len(t_hist), n_kv_heads, D)) * scale).astype(np.float32)
             slots = t_hist % self.ring if self.ring else t_hist
-            self._place(b, slots, kh, vh)
+            if v_int8:
+                codes, scales = O.quantize_v(vf)
+                self._place_k(self.k, b, slots, kh)
+                self._place_v8(self.v, self.vs, b, slots, codes, scales)
+                self.vc[b, slots] = O.dequantize_v(codes, scales)
+            else:
+                vh = O.to_bf16(vf)
+                self._place(b, slots, kh, vh)
+                self.vc[b, slots] = O.from_bf16(vh)
             self.kc[b, slots] = O.from_bf16(kh)
-            self.vc[b, slots] = O.from_bf16(vh)
 
         # The append, per the oracle.
         q_rot, _, kb, vb = O.kv_append(self.qkv, n_q_heads, n_kv_heads, self.cos, self.sin,
@@ -79,14 +99,34 @@ class DecodeCase:
         self.q_rot = q_rot
         self.k_expect = self.k.copy()
         self.v_expect = self.v.copy()
+        self.vs_expect = self.vs.copy() if v_int8 else None
+        v_new = self.qkv[:, (n_q_heads + n_kv_heads) * D:].reshape(B, n_kv_heads, D)
         for b in range(B):
             slot = int(self.pos[b] % self.ring) if self.ring else int(self.pos[b])
             phys = self.table[b, slot // BT]
             self.k_expect[phys, :, slot % BT, :] = kb[b]
-            self.v_expect[phys, :, :, slot % BT] = vb[b]
             self.kc[b, slot] = O.from_bf16(kb[b])
-            self.vc[b, slot] = O.from_bf16(vb[b])
+            if v_int8:
+                codes, scales = O.quantize_v(v_new[b])
+                self._place_v8(self.v_expect, self.vs_expect, b, np.array([slot]), codes[None],
+                               scales[None])
+                self.vc[b, slot] = O.dequantize_v(codes, scales)
+            else:
+                self.v_expect[phys, :, :, slot % BT] = vb[b]
+                self.vc[b, slot] = O.from_bf16(vb[b])
         del kvd
+
+    def _place_k(self, k, b, slots, kh):
+        phys = self.table[b, slots // BT]
+        k[phys, :, slots % BT, :] = kh
+
+    def _place_v8(self, v, vs, b, slots, codes, scales):
+        """codes [n, Hkv, 64] int8, scales [n, Hkv] -> the int8 block layout."""
+        for j, slot in enumerate(np.asarray(slots)):
+            phys = self.table[b, slot // BT]
+            t = int(slot % BT)
+            v[phys][:, v_int8_offsets(t)] = codes[j]
+            vs[phys, :, t] = scales[j]
 
     def _place(self, b, slots, kh, vh):
         phys = self.table[b, slots // BT]
@@ -113,7 +153,8 @@ class DecodeCase:
             "seq_lens": t(self.seq_lens),
             "table": t(self.table),
             "k": t(self.k.view(np.int16)),
-            "v": t(self.v.view(np.int16)),
+            "v": t(self.v) if self.v_int8 else t(self.v.view(np.int16)),
+            "vs": t(self.vs) if self.v_int8 else None,
             "err": torch.zeros(1, dtype=torch.int32, device=device),
         }
         return dev

@@ -22,7 +22,8 @@ def run_gpu(case: DecodeCase, gkv, torch, device, split_tokens=0, out_dtype=None
     if product_table:
         cos, sin = gkv.rope_table(case.cos.shape[0])
     dev = case.to_device(torch, device, cos, sin)
-    view = gkv.cache_view(dev["k"], dev["v"], dev["table"], case.Hkv, ring=case.ring)
+    view = gkv.cache_view(dev["k"], dev["v"], dev["table"], case.Hkv, ring=case.ring,
+                          v_scale=dev["vs"])
     q_out = None
     if not rotate_in_attention:
         q_out = torch.empty(case.B, case.Hq * 64, dtype=torch.float32, device=device)
@@ -49,7 +50,8 @@ def run_gpu(case: DecodeCase, gkv, torch, device, split_tokens=0, out_dtype=None
     torch.cuda.synchronize()
     res = {
         "k": dev["k"].cpu().numpy().view(np.uint16),
-        "v": dev["v"].cpu().numpy().view(np.uint16),
+        "v": dev["v"].cpu().numpy() if case.v_int8 else dev["v"].cpu().numpy().view(np.uint16),
+        "vs": dev["vs"].cpu().numpy() if case.v_int8 else None,
         "out": out.float().cpu().numpy().reshape(case.B, case.Hq, 64),
         "err": int(dev["err"].cpu().item()),
     }
@@ -62,6 +64,9 @@ def check_case(case, res, atol=ATOL, rtol=RTOL):
     assert res["err"] == 0
     assert np.array_equal(res["k"], case.k_expect), "K cache bytes differ"
     assert np.array_equal(res["v"], case.v_expect), "V cache bytes differ"
+    if case.v_int8:
+        assert np.array_equal(res["vs"].view(np.uint32), case.vs_expect.view(np.uint32)), \
+            "V scales differ"
     ref = case.oracle_out()
     assert np.isfinite(res["out"]).all()
     bad, worst = allclose_report(res["out"], ref, atol, rtol)
@@ -133,6 +138,28 @@ def test_decode_layer_call_matches_two_calls(gkv, cuda, torch_mod, window):
     check_case(case, fused)
     two = run_gpu(case, gkv, torch_mod, cuda)
     assert np.array_equal(fused["out"].view(np.uint32), two["out"].view(np.uint32))
+
+
+# ---- int8 V (the reference's quantized-V cache) ---------------------------------
+
+@pytest.mark.parametrize("window", [0, 128])
+def test_int8_v_cache(gkv, cuda, torch_mod, window):
+    """Append bit-exact (codes and scales of the reference's rule) and
+    attention within tolerance of the oracle on the dequantized values."""
+    rng = np.random.default_rng(70 + window)
+    B = 40
+    L = lens_uniform(rng, B, 0, 2100)
+    L[:4] = [0, 15, 127, 128]
+    case = DecodeCase(B, 64, 8, L, window=window, scale=0.5, seed=71 + window, v_int8=True)
+    check_case(case, run_gpu(case, gkv, torch_mod, cuda))
+    check_case(case, run_gpu(case, gkv, torch_mod, cuda, layer_call=True))
+
+
+def test_int8_v_config1_and_split_sizes(gkv, cuda, torch_mod):
+    L = np.array([1, 77, 200, 256], np.int32)
+    case = DecodeCase(4, 8, 2, L, window=0, scale=1.0, seed=72, v_int8=True)
+    for split in (0, 32, 128):
+        check_case(case, run_gpu(case, gkv, torch_mod, cuda, split_tokens=split))
 
 
 # ---- edges ---------------------------------------------------------------------

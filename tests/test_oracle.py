@@ -263,3 +263,42 @@ def test_oracle_rejects_bad_arguments():
         O.decode_attention(q, kc, kc, [10], np.zeros(8, np.float32))  # pos beyond cache
     with pytest.raises(ValueError):
         O.decode_attention(q, kc, kc, [-1], np.zeros(8, np.float32))
+
+
+def test_quantize_v_closed_forms():
+    """int8-V rule (fast_misc.hpp:74-84): codes of exact multiples of the
+    step, the amax element at +-127, ties to even, the all-zero head."""
+    step = np.float32(3.0) / np.float32(127.0)
+    k = np.arange(-63, 64, 2, dtype=np.float32)            # 64 values, amax at +-63
+    v = np.concatenate([k[:63], [127.0]]).astype(np.float32) * step
+    codes, scales = O.quantize_v(v.reshape(1, 64))
+    assert codes[0, -1] == 127 and np.isclose(scales[0], 3.0 / 127.0, rtol=1e-7)
+    assert np.array_equal(codes[0, :63], k[:63].astype(np.int8))
+    # amax = 127 makes the reciprocal exactly 1: x.5 values round to even
+    v = np.zeros(64, np.float32)
+    v[:6] = [127.0, 2.5, 3.5, -2.5, -3.5, 0.5]
+    codes, scales = O.quantize_v(v.reshape(1, 64))
+    assert list(codes[0, :6]) == [127, 2, 4, -2, -4, 0] and scales[0] == 1.0
+    codes, scales = O.quantize_v(np.zeros((2, 64), np.float32))
+    assert not codes.any() and not scales.any()
+    v = np.zeros(64, np.float32)
+    v[7] = -0.75
+    codes, scales = O.quantize_v(v.reshape(1, 64))
+    assert codes[0, 7] == -127 and scales[0] == np.float32(0.75) / np.float32(127.0)
+    # dequantized values stay within half a step of the input
+    rng = np.random.default_rng(5)
+    v = (rng.standard_normal((16, 64)) * 0.5).astype(np.float32)
+    codes, scales = O.quantize_v(v)
+    assert (np.abs(O.dequantize_v(codes, scales) - v) <= 0.5001 * scales[:, None]).all()
+
+
+@pytest.mark.skipif(not O.ref_q8_available(), reason="reference build absent")
+def test_quantize_v_matches_reference_build():
+    rng = np.random.default_rng(11)
+    for trial in range(200):
+        v = (rng.standard_normal(64) * rng.choice([1e-3, 0.5, 3.0, 1e4])).astype(np.float32)
+        if trial % 17 == 0:
+            v[:] = 0.0
+        codes, scales = O.quantize_v(v.reshape(1, 64))
+        rc, rs = O.ref_quantize_v(v)
+        assert np.array_equal(codes[0], rc) and np.float32(scales[0]) == np.float32(rs)
