@@ -23,6 +23,10 @@
  *       position (it is defined as that); brute force fp64 on tiny prompts.
  *   orc_kv_append  bit-exact vs run.cpp (_ref: the key written into the
  *       cache by forward()) and the bf16 rule above.
+ *   orc_quantize_v  bit-exact vs the reference's own quantize_v
+ *       (getp-csrc/tests/attn_test.cpp, built into oracle/_ref/libref_q8.so)
+ *       on random heads; closed forms: exact multiples of the step, the amax
+ *       element at +-127, ties to even, the all-zero head.
  */
 #include "kv_oracle.h"
 
