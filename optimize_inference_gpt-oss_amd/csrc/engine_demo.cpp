@@ -7,7 +7,8 @@
 //
 //   gkv_engine_demo <in.bin> <out.bin> [fused]
 // fused: the one-call form rope_kv_attention_bf16 instead of the two calls.
-// in.bin:  int32 P, B, Hq, Hkv, n_layers, window; fp32 qkv [P][n_layers][B][(Hq+2Hkv)*64];
+// in.bin:  int32 P, B, Hq, Hkv, n_layers, window, v_format (gkv_v_format);
+//          fp32 qkv [P][n_layers][B][(Hq+2Hkv)*64];
 //          fp32 sinks [n_layers][Hq]
 // out.bin: bf16 [P][n_layers][B][Hq*64] attention outputs of every step
 // Layer l is a window layer iff window > 0 and l is even (the pool's rule).
@@ -37,8 +38,8 @@ int main(int argc, char **argv) {
   FILE *f = fopen(argv[1], "rb");
   if (!f)
     return 2;
-  int32_t hdr[6];
-  if (fread(hdr, 4, 6, f) != 6)
+  int32_t hdr[7];
+  if (fread(hdr, 4, 7, f) != 7)
     return 2;
   const int P = hdr[0], B = hdr[1], Hq = hdr[2], Hkv = hdr[3], NL = hdr[4], W = hdr[5];
   const int QKV = (Hq + 2 * Hkv) * 64, ATT = Hq * 64;
@@ -57,6 +58,7 @@ int main(int argc, char **argv) {
   cfg.max_seq_len = P;
   cfg.num_blocks = (int64_t)B * ((P + 15) / 16) + 3;
   cfg.shuffle_seed = 77;
+  cfg.v_format = hdr[6];
   gkv_pool *pool = nullptr;
   gkv_engine::check(gkv_pool_create(&cfg, &pool), "gkv_pool_create");
   for (int b = 0; b < B; b++) {

@@ -19,8 +19,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 DEMO = os.path.join(ROOT, "optimize_inference_gpt-oss_amd", "gkv_engine_demo")
 
 
-@pytest.mark.parametrize("fused", [False, True])
-def test_engine_shim_decode_loop(oracle, cuda, tmp_path, fused):
+@pytest.mark.parametrize("fused,v_int8", [(False, False), (True, False), (True, True)])
+def test_engine_shim_decode_loop(oracle, cuda, tmp_path, fused, v_int8):
     if not os.path.exists(DEMO):
         pytest.fail("gkv_engine_demo is not built (run __graft_entry__.build())")
     P, B, Hq, Hkv, NL, W = 40, 3, 64, 8, 2, 32
@@ -29,7 +29,7 @@ def test_engine_shim_decode_loop(oracle, cuda, tmp_path, fused):
     sinks = rng.standard_normal((NL, Hq)).astype(np.float32)
     inp, outp = tmp_path / "in.bin", tmp_path / "out.bin"
     with open(inp, "wb") as f:
-        np.array([P, B, Hq, Hkv, NL, W], np.int32).tofile(f)
+        np.array([P, B, Hq, Hkv, NL, W, 1 if v_int8 else 0], np.int32).tofile(f)
         qkv.tofile(f)
         sinks.tofile(f)
     cmd = [DEMO, str(inp), str(outp)] + (["fused"] if fused else [])
@@ -47,7 +47,11 @@ def test_engine_shim_decode_loop(oracle, cuda, tmp_path, fused):
             pos = np.full(B, p, np.int32)
             q_rot, _, kb, vb = oracle.kv_append(qkv[p, l], Hq, Hkv, cos, sin, pos)
             kc[:, p] = oracle.from_bf16(kb)
-            vc[:, p] = oracle.from_bf16(vb)
+            if v_int8:
+                v_new = qkv[p, l][:, (Hq + Hkv) * 64:].reshape(B, Hkv, 64)
+                vc[:, p] = oracle.dequantize_v(*oracle.quantize_v(v_new))
+            else:
+                vc[:, p] = oracle.from_bf16(vb)
             ref = oracle.decode_attention(q_rot, kc[:, :p + 1], vc[:, :p + 1], pos, sinks[l],
                                           window=window)
             n_bad, max_err = allclose_report(got[p, l], ref, 2e-3, 1e-2 + 2 ** -8)
