@@ -103,7 +103,7 @@ def fill_cache(torch, gkv, pool, n_layers, dev, seed):
 
 
 def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, threads,
-                 min_seconds):
+                 min_seconds, layer_index=0):
     """Time the CPU oracle on a bounded sample of the workload: the attention of
     sequences 0..sample_seqs-1 of one layer over their cached K/V, repeated
     until min_seconds of wall time have passed; also checks the GPU output of
@@ -168,7 +168,7 @@ def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, th
     err = np.abs(got - ref)
     ok = bool(np.all(err <= 2e-3 + 1e-2 * np.abs(ref)))
     return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=threads, kind="port",
-                sample=f"{sample_seqs} sequences of layer 0 ({int(n_read.sum())} cached tokens, "
+                sample=f"{sample_seqs} sequences of layer {layer_index} ({int(n_read.sum())} cached tokens, "
                        f"{nbytes / 1e6:.1f} MB of K+V), one decode attention of one layer, "
                        f"{reps} passes, {dt:.3f} s wall per pass on {threads} OpenMP threads",
                 seconds=round(dt, 3), gpu_matches=ok, max_abs_err=float(err.max()))
@@ -495,7 +495,7 @@ def main() -> int:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         n_cpu = B if args.cpu_sample < 0 else min(args.cpu_sample, B)
         cpu = cpu_baseline(torch, gkv, pool, layers[full[0]], L, cfg, layers[full[0]].out,
-                           n_cpu, threads, args.cpu_seconds)
+                           n_cpu, threads, args.cpu_seconds, layer_index=full[0])
 
     value = kv_bytes / (ms_per_step * 1e-3) / 1e9
     line = {

@@ -70,19 +70,10 @@ constexpr int kPlanHeader = 4;         // ints: T, S, workgroups used, unused
 constexpr int kIdRegs = 4;             // block-id registers per wave: ranges of <= 4096 tokens
 constexpr int kMaxRange = kIdRegs * 64 * kBlockTokens;
 constexpr int kInfoRegs = kMaxRange / kStep / 64; // step-record registers
-#ifndef GKV_SPLIT_WAVES
-#define GKV_SPLIT_WAVES 4
-#endif
-constexpr int kSplitWaves = GKV_SPLIT_WAVES; // split kernel: waves per workgroup (4: one per SIMD)
+constexpr int kSplitWaves = 4;         // split kernel: one wave per SIMD
 constexpr int kSplitThreads = 64 * kSplitWaves;
 constexpr int kPrepThreads = 1024;
 constexpr int kMaxBatch = 8192;        // sequences per call (prefix sums kept in LDS)
-// Query operands are loaded only with the step that opens a segment (true), or
-// with every step (false).
-#ifndef GKV_Q_AT_SEGMENT_START
-#define GKV_Q_AT_SEGMENT_START 1
-#endif
-constexpr bool kQAtSegmentStart = GKV_Q_AT_SEGMENT_START;
 constexpr int kBadBlock = -1;          // F entry: id outside the pool
 constexpr int kPadBlock = -2;          // F entry: no tokens (padding)
 
@@ -329,7 +320,7 @@ __global__ __launch_bounds__(kPrepThreads) void decode_layer_prep_kernel(DecodeA
 // R: depth of the register ring of loaded steps (R - 1 steps in flight ahead
 // of the one being computed).
 template <int R, bool VQ>
-__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(kSplitWaves / 4)))
+__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(1)))
 void decode_split_kernel(DecodeArgs a) {
   constexpr int D = kHeadDim;
   const int w_id = blockIdx.x;
@@ -433,7 +424,7 @@ void decode_split_kernel(DecodeArgs a) {
         vr[nn] = u32x4{x[0], x[1], y[0], y[1]};
       }
     }
-    if (!kQAtSegmentStart || (rc & 0x80) || step == 0) {
+    if ((rc & 0x80) || step == 0) { // the step opens a segment: its query operands
       const u32x4 *qs = a.qops + (((int64_t)(rc >> 8) * a.n_kv_heads + g) * 64 + lane) * 2;
       qr[0] = qs[0];
       qr[1] = qs[1];
@@ -521,17 +512,15 @@ void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
       for (int nn = 0; nn < 4; nn++)
         o[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      if (kQAtSegmentStart) {
-        qcur[0] = qr[0];
-        qcur[1] = qr[1];
-      }
+      qcur[0] = qr[0];
+      qcur[1] = qr[1];
     }
     if (in_range)
       cur_ends = (rc & 0x40) != 0;
     const int valid = in_range ? (rc & 0x3f) : 0;
     const uint32_t bad = (uint32_t)bb & 3u;
-    const bf16x8 qop0 = __builtin_bit_cast(bf16x8, kQAtSegmentStart ? qcur[0] : qr[0]);
-    const bf16x8 qop1 = __builtin_bit_cast(bf16x8, kQAtSegmentStart ? qcur[1] : qr[1]);
+    const bf16x8 qop0 = __builtin_bit_cast(bf16x8, qcur[0]);
+    const bf16x8 qop1 = __builtin_bit_cast(bf16x8, qcur[1]);
     // Scores of token 4*kg + r of block jt (slot 4*jt + r), this lane's column.
     float sc[8];
 #pragma unroll
