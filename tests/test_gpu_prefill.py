@@ -12,7 +12,7 @@ rel 1e-2 (bf16 K/V, fp32 accumulate).
 import numpy as np
 import pytest
 
-from kvcase import allclose_report
+from kvcase import INT8_POISON, allclose_report, v_int8_offsets
 
 pytestmark = pytest.mark.gpu
 
@@ -22,8 +22,10 @@ NAN16 = np.uint16(0x7FC1)
 
 
 class PrefillCase:
-    def __init__(self, oracle, seed, lengths, Hq, Hkv, window=0, scale=0.5, sink_scale=1.0):
+    def __init__(self, oracle, seed, lengths, Hq, Hkv, window=0, scale=0.5, sink_scale=1.0,
+                 v_int8=False):
         rng = np.random.default_rng(seed)
+        self.v_int8 = v_int8
         self.L = np.asarray(lengths, np.int64)
         self.B = len(self.L)
         self.Hq, self.Hkv, self.window = Hq, Hkv, window
@@ -51,7 +53,13 @@ class PrefillCase:
             self.table[b, :nb] = perm[i:i + nb]
             i += nb
         self.k_expect = np.full((self.NB, Hkv, 16, D), NAN16, np.uint16)
-        self.v_expect = np.full((self.NB, Hkv, D, 16), NAN16, np.uint16)
+        if v_int8:
+            self.v_expect = np.full((self.NB, Hkv, 16 * D), INT8_POISON, np.int8)
+            self.vs_expect = np.full((self.NB, Hkv, 16), np.nan, np.float32)
+            v_rows = self.qkv[:, (Hq + Hkv) * D:].reshape(T, Hkv, D)
+            codes, scales = oracle.quantize_v(v_rows)
+        else:
+            self.v_expect = np.full((self.NB, Hkv, D, 16), NAN16, np.uint16)
         for r in range(T):
             b, p = int(self.row_seq[r]), int(self.pos[r])
             if window and p + window < self.L[b]:
@@ -59,7 +67,11 @@ class PrefillCase:
             slot = p % window if window else p
             blk, off = self.table[b, slot // 16], slot % 16
             self.k_expect[blk, :, off, :] = self.kb[r]
-            self.v_expect[blk, :, :, off] = self.vb[r]
+            if v_int8:
+                self.v_expect[blk][:, v_int8_offsets(off)] = codes[r]
+                self.vs_expect[blk, :, off] = scales[r]
+            else:
+                self.v_expect[blk, :, :, off] = self.vb[r]
 
     def oracle_out(self):
         from oracle import kv_oracle as O
@@ -72,9 +84,14 @@ def run_gpu(case, gkv, torch, dev, out_dtype=None, ring=True):
     qkv = t(case.qkv)
     cos, sin = gkv.rope_table(max(case.max_len, 1))
     k = t(np.full((case.NB, case.Hkv, 16, D), NAN16, np.uint16).view(np.int16))
-    v = t(np.full((case.NB, case.Hkv, D, 16), NAN16, np.uint16).view(np.int16))
+    vs = None
+    if case.v_int8:
+        v = t(np.full((case.NB, case.Hkv, 16 * D), INT8_POISON, np.int8))
+        vs = t(np.full((case.NB, case.Hkv, 16), np.nan, np.float32))
+    else:
+        v = t(np.full((case.NB, case.Hkv, D, 16), NAN16, np.uint16).view(np.int16))
     table = t(case.table)
-    view = gkv.cache_view(k, v, table, case.Hkv, ring=case.window if ring else 0)
+    view = gkv.cache_view(k, v, table, case.Hkv, ring=case.window if ring else 0, v_scale=vs)
     T = max(case.T, 1)
     q_out = torch.full((T, case.Hq * D), float("nan"), dtype=torch.float32, device=dev)
     k_pack = torch.zeros((T, case.Hkv * D), dtype=torch.int16, device=dev)
@@ -93,7 +110,9 @@ def run_gpu(case, gkv, torch, dev, out_dtype=None, ring=True):
         q=q_out.cpu().numpy()[:case.T].reshape(case.T, case.Hq, D),
         kp=k_pack.cpu().numpy().view(np.uint16)[:case.T].reshape(case.T, case.Hkv, D),
         vp=v_pack.cpu().numpy().view(np.uint16)[:case.T].reshape(case.T, case.Hkv, D),
-        k=k.cpu().numpy().view(np.uint16), v=v.cpu().numpy().view(np.uint16),
+        k=k.cpu().numpy().view(np.uint16),
+        v=v.cpu().numpy() if case.v_int8 else v.cpu().numpy().view(np.uint16),
+        vs=vs.cpu().numpy() if case.v_int8 else None,
         out=out.float().cpu().numpy()[:case.T].reshape(case.T, case.Hq, D))
 
 
@@ -104,6 +123,9 @@ def check(case, res, atol=ATOL, rtol=RTOL):
     assert np.array_equal(res["vp"], case.vb), "packed V bits"
     assert np.array_equal(res["k"], case.k_expect), "K cache bytes differ"
     assert np.array_equal(res["v"], case.v_expect), "V cache bytes differ"
+    if case.v_int8:
+        assert np.array_equal(res["vs"].view(np.uint32), case.vs_expect.view(np.uint32)), \
+            "V scales differ"
     ref = case.oracle_out()
     n_bad, max_err = allclose_report(res["out"], ref, atol, rtol)
     assert n_bad == 0, f"{n_bad} outputs outside tolerance, max abs err {max_err}"
@@ -143,6 +165,16 @@ def test_large_scores_bf16_out(oracle, gkv, cuda):
     ref = case.oracle_out()
     n_bad, max_err = allclose_report(res["out"], ref, ATOL, RTOL + 2 ** -8)  # + bf16 output rounding
     assert n_bad == 0, f"{n_bad} outputs outside tolerance, max abs err {max_err}"
+
+
+@pytest.mark.parametrize("window", [0, 128])
+def test_prompt_append_into_int8_v_cache(oracle, gkv, cuda, window):
+    """Whole prompts appended into an int8-V cache: codes and scales of every
+    stored row bit-exact (ring: the last W positions), packed K/V unchanged."""
+    import torch
+    case = PrefillCase(oracle, 90 + window, [1, 16, 130, 300], 64, 8, window=window,
+                       v_int8=True)
+    check(case, run_gpu(case, gkv, torch, cuda))
 
 
 def test_empty_batch_and_zero_length(oracle, gkv, cuda):
