@@ -115,7 +115,9 @@ def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, th
     v = layer_state.view
     n_blk_total = v.num_blocks
     # gather the sampled sequences' logical caches to the host
+    idx = lambda kind: torch.tensor(gkv.block_offsets(kind), device="cuda").reshape(-1)  # noqa: E731
     k_arr = gkv_cache_tensor(torch, v.k, n_blk_total, Hkv, (16, D))
+    k_arr = k_arr.view(n_blk_total, Hkv, 16 * D)[:, :, idx("k")].view(n_blk_total, Hkv, 16, D)
     v_int8 = v.v_format == gkv.V_INT8
     if v_int8:
         # int8 codes and scales, dequantized to fp32 [block, head, dim, token]
@@ -125,15 +127,12 @@ def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, th
         scl = torch.empty(n // D, dtype=torch.float32, device="cuda")
         gkv.hip_memcpy_d2d(scl.data_ptr(), v.v_scale, n // D * 4)
         torch.cuda.synchronize()
-        d = torch.arange(D, device="cuda")
-        t16 = torch.arange(16, device="cuda")
-        off = ((d[:, None] % 16) * 4 + t16[None, :] // 4) * 16 + (d[:, None] // 16) * 4 \
-            + t16[None, :] % 4                                   # [dim, token]
-        codes = codes.view(n_blk_total, Hkv, 16 * D)[:, :, off.reshape(-1)]
+        codes = codes.view(n_blk_total, Hkv, 16 * D)[:, :, idx("v_int8")]   # [dim, token]
         v_arr = (codes.float().view(n_blk_total, Hkv, D, 16)
                  * scl.view(n_blk_total, Hkv, 1, 16))
     else:
         v_arr = gkv_cache_tensor(torch, v.v, n_blk_total, Hkv, (D, 16))
+        v_arr = v_arr.view(n_blk_total, Hkv, 16 * D)[:, :, idx("v")].view(n_blk_total, Hkv, D, 16)
     table = table_tensor(torch, v, sample_seqs)
     seq_lens = (L[:sample_seqs] + 1).astype(np.int32)
     W = layer_state.window

@@ -28,8 +28,12 @@
  * Layouts (device memory):
  *   qkv rows     fp32 [Q (Hq*64) | K (Hkv*64) | V (Hkv*64)], row stride in floats
  *                (fast_misc.hpp:57-58)
- *   K cache      bf16 [num_blocks][Hkv][block_tokens=16][64]
- *   V cache      bf16 [num_blocks][Hkv][64][16]  (transposed inside a block)
+ *   K cache      bf16 [num_blocks][Hkv][1024]: token t, dim d of a 16-token block at
+ *                element (d/32)*512 + ((d%32)/8*16 + t)*8 + d%8
+ *   V cache      bf16 [num_blocks][Hkv][1024]: token t, dim d at element
+ *                (d/32)*512 + ((t/4)*16 + d%16)*8 + ((d/16)%2)*4 + t%4
+ *                (both put each lane's matrix-core operand in 16 contiguous bytes,
+ *                in lane order; gkv.py block_offsets() tabulates them)
  *   block table  int32 [B][table_stride]: logical block j of sequence b -> physical block
  *   ring layers  (sliding window W, W % 16 == 0): position p lives in slot p % W, the
  *                table row holds W/16 blocks (gpu_engine.hpp:477, misc.hpp:72-85)
@@ -68,8 +72,9 @@ typedef enum { GKV_V_BF16 = 0, GKV_V_INT8 = 1 } gkv_v_format;
 
 /* A paged cache of one layer as the kernels see it. */
 typedef struct {
-  void *k;                     /* bf16 [num_blocks][n_kv_heads][16][64] */
-  void *v;                     /* GKV_V_BF16: bf16 [num_blocks][n_kv_heads][64][16];
+  void *k;                     /* bf16 [num_blocks][n_kv_heads][1024] (K block layout) */
+  void *v;                     /* GKV_V_BF16: bf16 [num_blocks][n_kv_heads][1024] (V block
+                                  layout);
                                   GKV_V_INT8: int8 [num_blocks][n_kv_heads][1024], code of
                                   dim d, token t at ((d % 16) * 4 + t / 4) * 16 + (d / 16) * 4
                                   + t % 4 */

@@ -44,11 +44,13 @@
 //   A step is 2 blocks (32 tokens); score tile jt is block jt, row m token m,
 //   so lane (kg = lane/16, col) holds the scores of tokens 4kg..4kg+3 of each
 //   block -- exactly its P^T operand slots, whose V^T operand is the same 4
-//   tokens of one dim: an 8-byte piece of each transposed V block. No
+//   tokens of one dim. The pool's block layouts (k_offset / v_offset) store
+//   each lane's operand pieces as 16 contiguous bytes in lane order, so every
+//   load instruction reads 1 KB contiguous: whole 128-byte lines. No
 //   register transposes, no LDS.
 //
-// Memory: raw buffer loads, one block of one head per instruction (scalar
-// base, constant per-lane offset, 2 KB range); R - 1 steps (8 KB of K/V
+// Memory: raw nontemporal buffer loads, half a block of one head per
+// instruction (scalar base, constant per-lane offset); R - 1 steps (8 KB of K/V
 // each) in flight per wave, held in VGPRs and AGPRs (one wave per SIMD: two
 // waves on a SIMD are not served equally, the older one issues first, which
 // leaves the younger ones running alone at the end). Every load is
@@ -61,6 +63,11 @@
 
 namespace gkv {
 
+// Cache policy of the K/V loads: nontemporal (the cache is read once per
+// step). Measured on the MI355X, a gather of random 2 KB blocks reads 6.9 TB/s
+// with it against 6.1 TB/s without, provided each load instruction covers
+// whole 128-byte lines (1 KB contiguous per wave).
+constexpr int kKvAux = 2;
 constexpr int kStep = 32;              // tokens per wave step
 constexpr int kCols = 8;               // query heads per kv head handled (G <= 8)
 constexpr int kMlStride = 16;          // floats of (m, l) per partial: 8 heads x 2
@@ -340,8 +347,9 @@ void decode_split_kernel(DecodeArgs a) {
   const bool head_ok = head < a.G;
 
   // Per-lane load offsets (bytes), the same for every step.
-  const uint32_t k_off = (uint32_t)(col * D + 8 * kg) * 2;
-  const uint32_t v_off = (uint32_t)(col * kBlockTokens + 4 * kg) * 2; // + nn * 512
+  // K and V: one 16-byte piece per lane of each 1 KB half of a head's block
+  // (the block layouts k_offset / v_offset put them in lane order).
+  const uint32_t kv_off = (uint32_t)lane * 16;
   const size_t head_bytes = (size_t)kBlockTokens * D * 2;               // 2 KB
   const uint32_t vq_off = (uint32_t)(col * 4 + kg) * 16;                 // int8 V piece
 
@@ -399,10 +407,10 @@ void decode_split_kernel(DecodeArgs a) {
     const __amdgpu_buffer_rsrc_t k1 = head_rsrc((const char *)a.kc + h1);
     const __amdgpu_buffer_rsrc_t v0 = head_rsrc((const char *)a.vc + h0);
     const __amdgpu_buffer_rsrc_t v1 = head_rsrc((const char *)a.vc + h1);
-    kr[0] = __builtin_amdgcn_raw_buffer_load_b128(k0, k_off, 0, 0);
-    kr[1] = __builtin_amdgcn_raw_buffer_load_b128(k0, k_off + 64, 0, 0);
-    kr[2] = __builtin_amdgcn_raw_buffer_load_b128(k1, k_off, 0, 0);
-    kr[3] = __builtin_amdgcn_raw_buffer_load_b128(k1, k_off + 64, 0, 0);
+    kr[0] = __builtin_amdgcn_raw_buffer_load_b128(k0, kv_off, 0, kKvAux);
+    kr[1] = __builtin_amdgcn_raw_buffer_load_b128(k0, kv_off + 1024, 0, kKvAux);
+    kr[2] = __builtin_amdgcn_raw_buffer_load_b128(k1, kv_off, 0, kKvAux);
+    kr[3] = __builtin_amdgcn_raw_buffer_load_b128(k1, kv_off + 1024, 0, kKvAux);
     if (VQ) {
       // int8 V: one 16-byte piece per block (dims col + 16nn, tokens
       // 4kg..4kg+3), then the 4 scales of those tokens per block
@@ -412,16 +420,19 @@ void decode_split_kernel(DecodeArgs a) {
       const __amdgpu_buffer_rsrc_t c1 = head_rsrc((const char *)a.vc + q1);
       const __amdgpu_buffer_rsrc_t s0 = head_rsrc((const char *)a.vs + q0 / 16);
       const __amdgpu_buffer_rsrc_t s1 = head_rsrc((const char *)a.vs + q1 / 16);
-      vr[0] = __builtin_amdgcn_raw_buffer_load_b128(c0, vq_off, 0, 0);
-      vr[1] = __builtin_amdgcn_raw_buffer_load_b128(c1, vq_off, 0, 0);
-      vr[2] = __builtin_amdgcn_raw_buffer_load_b128(s0, 16 * kg, 0, 0);
-      vr[3] = __builtin_amdgcn_raw_buffer_load_b128(s1, 16 * kg, 0, 0);
+      vr[0] = __builtin_amdgcn_raw_buffer_load_b128(c0, vq_off, 0, kKvAux);
+      vr[1] = __builtin_amdgcn_raw_buffer_load_b128(c1, vq_off, 0, kKvAux);
+      vr[2] = __builtin_amdgcn_raw_buffer_load_b128(s0, 16 * kg, 0, kKvAux);
+      vr[3] = __builtin_amdgcn_raw_buffer_load_b128(s1, 16 * kg, 0, kKvAux);
     } else {
+      // half h of each block: tokens 4kg..4kg+3 of dims col + 32h and
+      // col + 32h + 16; operand nn takes its 4 tokens from each block
 #pragma unroll
-      for (int nn = 0; nn < 4; nn++) {
-        const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(v0, v_off + nn * 512, 0, 0);
-        const u32x2 y = __builtin_amdgcn_raw_buffer_load_b64(v1, v_off + nn * 512, 0, 0);
-        vr[nn] = u32x4{x[0], x[1], y[0], y[1]};
+      for (int h = 0; h < 2; h++) {
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(v0, kv_off + h * 1024, 0, kKvAux);
+        const u32x4 y = __builtin_amdgcn_raw_buffer_load_b128(v1, kv_off + h * 1024, 0, kKvAux);
+        vr[2 * h] = u32x4{x[0], x[1], y[0], y[1]};
+        vr[2 * h + 1] = u32x4{x[2], x[3], y[2], y[3]};
       }
     }
     if ((rc & 0x80) || step == 0) { // the step opens a segment: its query operands

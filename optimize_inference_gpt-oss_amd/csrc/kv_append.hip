@@ -9,9 +9,10 @@
 // (gkv_rope_table), so the stored bits equal the CPU path's bf16 of its fp32
 // key.
 //
-// Layout written: K [block][head][16 tokens][64], V [block][head][64][16]
-// (V transposed inside its block so that the attention kernel's PV operand is
-// one 16-byte load per lane). One workgroup per row; HBM-bound and tiny
+// Layout written: 2 KB per block and head for K and for V, in the orders of
+// k_offset / v_offset (kv_append.hpp), which put each lane's matrix-core
+// operand pieces of the attention kernel in 16 contiguous bytes, in lane
+// order. One workgroup per row; HBM-bound and tiny
 // (2 KB written per token per layer).
 #include "kv_append.hpp"
 

@@ -23,6 +23,21 @@ struct AppendArgs {
   int v_int8;  // 1: V is stored as int8 codes + scales (gkv_v_format GKV_V_INT8)
 };
 
+// Element offset of token t, dim d inside one head's bf16 K block (16 x 64
+// values, 2 KB): [d / 32][(d % 32) / 8][t][d % 8]. Lane kg * 16 + t of the
+// attention kernel holds dims 32m + 8kg .. +7 of token t for its m-th matrix
+// op, so each 1 KB half is one 16-byte load per lane in lane order.
+__host__ __device__ __forceinline__ int k_offset(int t, int d) {
+  return (d / 32) * 512 + ((d % 32) / 8 * 16 + t) * 8 + d % 8;
+}
+
+// Element offset of token t, dim d inside one head's bf16 V block (2 KB):
+// [d / 32][t / 4][d % 16][(d / 16) % 2][t % 4]. Lane kg * 16 + i finds tokens
+// 4kg .. 4kg+3 of dims i + 32h and i + 32h + 16 in one 16-byte piece of half h.
+__host__ __device__ __forceinline__ int v_offset(int t, int d) {
+  return (d / 32) * 512 + ((t / 4) * 16 + d % 16) * 8 + ((d / 16) % 2) * 4 + t % 4;
+}
+
 // Offset of dim d, token t inside one head's 1 KB int8 V block: lane (kg, i)
 // of the attention kernel finds the codes of dims i, i+16, i+32, i+48 for
 // tokens 4kg..4kg+3 in one 16-byte piece.
@@ -87,9 +102,9 @@ __device__ __forceinline__ void append_row(const AppendArgs &a, int r, int tid, 
     const uint16_t k1 = f32_to_bf16_rne(rope_first(x1, x2, c, s));
     const uint16_t k2 = f32_to_bf16_rne(rope_second(x1, x2, c, s));
     if (store) {
-      uint16_t *kd = a.kc + kbase + ((int64_t)g * kBlockTokens + off) * D;
-      kd[i] = k1;
-      kd[HALF + i] = k2;
+      uint16_t *kd = a.kc + kbase + (int64_t)g * (kBlockTokens * D);
+      kd[k_offset(off, i)] = k1;
+      kd[k_offset(off, HALF + i)] = k2;
     }
     if (a.k_pack) {
       uint16_t *kp = a.k_pack + (int64_t)r * kv_dim + g * D;
@@ -125,7 +140,7 @@ __device__ __forceinline__ void append_row(const AppendArgs &a, int r, int tid, 
     const int g = idx / D, d = idx % D;
     const uint16_t v = f32_to_bf16_rne(vr[idx]);
     if (store)
-      a.vc[vbase + ((int64_t)g * D + d) * kBlockTokens + off] = v;
+      a.vc[vbase + (int64_t)g * (kBlockTokens * D) + v_offset(off, d)] = v;
     if (a.v_pack)
       a.v_pack[(int64_t)r * kv_dim + idx] = v;
   }

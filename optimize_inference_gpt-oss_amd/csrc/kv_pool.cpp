@@ -6,8 +6,8 @@
 // gpu_alloc_state :316-334 with slots = max_pos or the window, rounded to 64)
 // by 16-token blocks handed out from a free list:
 //   full layers    one block id covers 16 positions of a sequence in every full
-//                  layer; per layer K [num_blocks][Hkv][16][64] and
-//                  V [num_blocks][Hkv][64][16], bf16 (32 KB per block at Hkv=8)
+//                  layer; per layer K and V [num_blocks][Hkv][1024] bf16 in
+//                  the block layouts of kv_append.hpp (32 KB per block at Hkv=8)
 //   window layers  a ring of W/16 blocks per sequence id, fixed at create time
 //                  (the reference's slots = window, gpu_engine.hpp:318-319)
 //   tables         int32 [max_seqs][ceil(max_seq_len/16)] and [max_seqs][W/16],

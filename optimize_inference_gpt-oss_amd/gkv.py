@@ -42,6 +42,24 @@ class CacheView(ctypes.Structure):
 V_BF16, V_INT8 = 0, 1
 
 
+def block_offsets(kind: str):
+    """Element offsets inside one head's block of the pool (as the kernels in
+    csrc/kv_append.hpp lay it out), as nested lists:
+    - "k": [16 tokens][64 dims] of the bf16 K block (2 KB),
+    - "v": [64 dims][16 tokens] of the bf16 V block (2 KB),
+    - "v_int8": [64 dims][16 tokens] of the int8 V block (1 KB)."""
+    if kind == "k":
+        return [[(d // 32) * 512 + ((d % 32) // 8 * 16 + t) * 8 + d % 8 for d in range(64)]
+                for t in range(16)]
+    if kind == "v":
+        return [[(d // 32) * 512 + ((t // 4) * 16 + d % 16) * 8 + ((d // 16) % 2) * 4 + t % 4
+                 for t in range(16)] for d in range(64)]
+    if kind == "v_int8":
+        return [[((d % 16) * 4 + t // 4) * 16 + (d // 16) * 4 + t % 4 for t in range(16)]
+                for d in range(64)]
+    raise ValueError(f"unknown block kind {kind!r}")
+
+
 class RopeConfig(ctypes.Structure):
     _fields_ = [("base", _f), ("head_dim", _i32), ("scaling_factor", _f),
                 ("initial_context_length", _f), ("ntk_beta", _f), ("ntk_alpha", _f)]

@@ -23,6 +23,44 @@ def v_int8_offsets(t):
     return ((d % 16) * 4 + t // 4) * 16 + (d // 16) * 4 + t % 4
 
 
+def k_block_offsets():
+    """[16, 64]: element offset of (token t, dim d) in a head's bf16 K block.
+    Lane kg*16 + t of the attention kernel loads 8 elements at lane*8 (+512 for
+    dims 32..63): dims 32m + 8kg .. +7 of token t."""
+    t = np.arange(BT)[:, None]
+    d = np.arange(D)[None, :]
+    return (d // 32) * 512 + ((d % 32) // 8 * 16 + t) * 8 + d % 8
+
+
+def v_block_offsets():
+    """[64, 16]: element offset of (dim d, token t) in a head's bf16 V block.
+    Lane kg*16 + i loads 8 elements at lane*8 (+512 for half h): tokens
+    4kg .. 4kg+3 of dim i + 32h, then of dim i + 32h + 16."""
+    d = np.arange(D)[:, None]
+    t = np.arange(BT)[None, :]
+    return (d // 32) * 512 + ((t // 4) * 16 + d % 16) * 8 + ((d // 16) % 2) * 4 + t % 4
+
+
+_K_OFF = k_block_offsets().reshape(-1)
+_V_OFF = v_block_offsets().reshape(-1)
+
+
+def to_pool(x, kind):
+    """Logical blocks ([..., 16, 64] K or [..., 64, 16] V) -> pool bytes [..., 1024]."""
+    off = _K_OFF if kind == "k" else _V_OFF
+    out = np.empty(x.shape[:-2] + (BT * D,), x.dtype)
+    out[..., off] = x.reshape(x.shape[:-2] + (BT * D,))
+    return out
+
+
+def from_pool(p, kind):
+    """Pool bytes [..., 1024] (or any [..., 16, 64]-sized trailing dims) -> logical blocks."""
+    p = p.reshape(p.shape[:-2] + (BT * D,)) if p.shape[-1] != BT * D else p
+    off = _K_OFF if kind == "k" else _V_OFF
+    shape = (BT, D) if kind == "k" else (D, BT)
+    return p[..., off].reshape(p.shape[:-1] + shape)
+
+
 class DecodeCase:
     def __init__(self, B, n_q_heads, n_kv_heads, ctx_lens, window=0, scale=1.0, seed=0,
                  extra_blocks=7, rope_rows=None, sink_scale=1.0, v_int8=False):
@@ -152,8 +190,8 @@ class DecodeCase:
             "pos": t(self.pos),
             "seq_lens": t(self.seq_lens),
             "table": t(self.table),
-            "k": t(self.k.view(np.int16)),
-            "v": t(self.v) if self.v_int8 else t(self.v.view(np.int16)),
+            "k": t(to_pool(self.k, "k").view(np.int16)),
+            "v": t(self.v) if self.v_int8 else t(to_pool(self.v, "v").view(np.int16)),
             "vs": t(self.vs) if self.v_int8 else None,
             "err": torch.zeros(1, dtype=torch.int32, device=device),
         }

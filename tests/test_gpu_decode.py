@@ -9,7 +9,7 @@ north-star contract. Inputs are seeded; shapes follow the BASELINE configs
 import numpy as np
 import pytest
 
-from kvcase import DecodeCase, allclose_report
+from kvcase import DecodeCase, allclose_report, from_pool
 
 pytestmark = pytest.mark.gpu
 
@@ -49,8 +49,9 @@ def run_gpu(case: DecodeCase, gkv, torch, device, split_tokens=0, out_dtype=None
                              dev_err=dev["err"])
     torch.cuda.synchronize()
     res = {
-        "k": dev["k"].cpu().numpy().view(np.uint16),
-        "v": dev["v"].cpu().numpy() if case.v_int8 else dev["v"].cpu().numpy().view(np.uint16),
+        "k": from_pool(dev["k"].cpu().numpy().view(np.uint16), "k"),
+        "v": dev["v"].cpu().numpy() if case.v_int8 else
+        from_pool(dev["v"].cpu().numpy().view(np.uint16), "v"),
         "vs": dev["vs"].cpu().numpy() if case.v_int8 else None,
         "out": out.float().cpu().numpy().reshape(case.B, case.Hq, 64),
         "err": int(dev["err"].cpu().item()),

@@ -12,7 +12,7 @@ rel 1e-2 (bf16 K/V, fp32 accumulate).
 import numpy as np
 import pytest
 
-from kvcase import INT8_POISON, allclose_report, v_int8_offsets
+from kvcase import INT8_POISON, allclose_report, from_pool, v_int8_offsets
 
 pytestmark = pytest.mark.gpu
 
@@ -110,8 +110,8 @@ def run_gpu(case, gkv, torch, dev, out_dtype=None, ring=True):
         q=q_out.cpu().numpy()[:case.T].reshape(case.T, case.Hq, D),
         kp=k_pack.cpu().numpy().view(np.uint16)[:case.T].reshape(case.T, case.Hkv, D),
         vp=v_pack.cpu().numpy().view(np.uint16)[:case.T].reshape(case.T, case.Hkv, D),
-        k=k.cpu().numpy().view(np.uint16),
-        v=v.cpu().numpy() if case.v_int8 else v.cpu().numpy().view(np.uint16),
+        k=from_pool(k.cpu().numpy().view(np.uint16), "k"),
+        v=v.cpu().numpy() if case.v_int8 else from_pool(v.cpu().numpy().view(np.uint16), "v"),
         vs=vs.cpu().numpy() if case.v_int8 else None,
         out=out.float().cpu().numpy()[:case.T].reshape(case.T, case.Hq, D))
 
