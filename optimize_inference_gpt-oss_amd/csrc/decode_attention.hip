@@ -203,11 +203,20 @@ __device__ void prep_queries(const DecodeArgs &a, int item) {
   dst[1] = __builtin_bit_cast(u32x4, pack_pieces(qb, lo));
 }
 
-// Every workgroup computes the prefix sums in LDS (the lengths are 4 bytes per
-// sequence, cheap to read again), then takes its share of the stream blocks
-// and of the query items; workgroup 0 also publishes the plan. wg / n_wgs:
-// this workgroup's index among the prep workgroups and their count.
-__device__ __forceinline__ void prep_body(const DecodeArgs &a, int wg, int n_wgs) {
+// Query operands: one wave per (sequence, kv head). wg / n_wgs: this
+// workgroup's index among the query workgroups and their count.
+__device__ __forceinline__ void prep_query_items(const DecodeArgs &a, int wg, int n_wgs) {
+  const int waves = kPrepThreads / 64;
+  for (int item = wg * waves + (threadIdx.x >> 6); item < a.B * a.n_kv_heads;
+       item += n_wgs * waves)
+    prep_queries(a, item);
+}
+
+// Every block workgroup computes the prefix sums in LDS (the lengths are 4
+// bytes per sequence, cheap to read again), then takes its share of the
+// stream blocks; workgroup 0 also publishes the plan. wg / n_wgs: this
+// workgroup's index among the block workgroups and their count.
+__device__ __forceinline__ void prep_blocks(const DecodeArgs &a, int wg, int n_wgs) {
   __shared__ int s_cu[kMaxBatch + 1];
   __shared__ int s_scan[2][kPrepThreads];
   const int t = threadIdx.x, B = a.B;
@@ -292,34 +301,40 @@ __device__ __forceinline__ void prep_body(const DecodeArgs &a, int wg, int n_wgs
   }
   if (any_bad && a.dev_err)
     atomicOr(a.dev_err, GKV_DEVERR_BLOCK_ID);
-
-  // Query operands: one wave per (sequence, kv head).
-  const int waves = kPrepThreads / 64;
-  for (int item = wg * waves + (t >> 6); item < B * a.n_kv_heads; item += n_wgs * waves)
-    prep_queries(a, item);
 }
 
-__global__ __launch_bounds__(kPrepThreads) void decode_prep_kernel(DecodeArgs a) {
-  prep_body(a, blockIdx.x, gridDim.x);
+// Workgroups 0 .. n_qwg-1 prepare the query operands, the others the plan
+// and the stream blocks: the two chains (query loads; lengths, prefix sums,
+// table loads) run side by side.
+__global__ __launch_bounds__(kPrepThreads) void decode_prep_kernel(DecodeArgs a, int n_qwg) {
+  if ((int)blockIdx.x < n_qwg)
+    prep_query_items(a, blockIdx.x, n_qwg);
+  else
+    prep_blocks(a, blockIdx.x - n_qwg, gridDim.x - n_qwg);
 }
 
 // The append of a decode layer (row b = the new token of sequence b, at
 // position seq_lens[b] - 1) and the prepare work in one launch: workgroups
-// 0 .. n_app-1 append 4 rows each (256 threads per row), the others run
-// prep_body. The two parts touch disjoint memory (the prepare reads the raw
-// query of the qkv rows, the block tables and the lengths).
+// 0 .. n_app-1 append 4 rows each (256 threads per row), the next n_qwg
+// prepare the query operands, the others the plan and the stream blocks. The
+// parts touch disjoint memory (the prepare reads the raw query of the qkv
+// rows, the block tables and the lengths).
 constexpr int kAppendRowsPerWg = kPrepThreads / 256;
 __global__ __launch_bounds__(kPrepThreads) void decode_layer_prep_kernel(DecodeArgs a,
                                                                          AppendArgs ap,
                                                                          int n_rows,
-                                                                         int n_app) {
-  if ((int)blockIdx.x < n_app) {
-    const int r = blockIdx.x * kAppendRowsPerWg + (threadIdx.x >> 8);
+                                                                         int n_app,
+                                                                         int n_qwg) {
+  const int wg = blockIdx.x;
+  if (wg < n_app) {
+    const int r = wg * kAppendRowsPerWg + (threadIdx.x >> 8);
     if (r < n_rows)
       append_row(ap, r, threadIdx.x & 255, 256);
-    return;
+  } else if (wg < n_app + n_qwg) {
+    prep_query_items(a, wg - n_app, n_qwg);
+  } else {
+    prep_blocks(a, wg - n_app - n_qwg, gridDim.x - n_app - n_qwg);
   }
-  prep_body(a, blockIdx.x - n_app, gridDim.x - n_app);
 }
 
 // ---- split ----------------------------------------------------------------------
@@ -856,24 +871,32 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
   return GKV_OK;
 }
 
-static int prep_workgroups(const DecodeArgs &a, int64_t t_max) {
+// Query workgroups (one wave per item) and block workgroups (one thread per
+// 16-token block of the longest possible stream), each at most 1024.
+static int query_workgroups(const DecodeArgs &a) {
   const int waves = kPrepThreads / 64;
-  const int64_t by_items = (a.B * a.n_kv_heads + waves - 1) / waves;
-  const int64_t by_blocks = (t_max / kBlockTokens + kPrepThreads - 1) / kPrepThreads;
-  return (int)std::max<int64_t>(1, std::min<int64_t>(1024, std::max(by_items, by_blocks)));
+  return (int)std::max<int64_t>(
+      1, std::min<int64_t>(1024, ((int64_t)a.B * a.n_kv_heads + waves - 1) / waves));
+}
+
+static int block_workgroups(int64_t t_max) {
+  return (int)std::max<int64_t>(
+      1, std::min<int64_t>(1024, (t_max / kBlockTokens + kPrepThreads - 1) / kPrepThreads));
 }
 
 static int launch_prep(const DecodeArgs &a, int64_t t_max, hipStream_t s) {
-  hipLaunchKernelGGL(decode_prep_kernel, dim3(prep_workgroups(a, t_max)), dim3(kPrepThreads), 0,
-                     s, a);
+  const int n_qwg = query_workgroups(a);
+  hipLaunchKernelGGL(decode_prep_kernel, dim3(n_qwg + block_workgroups(t_max)),
+                     dim3(kPrepThreads), 0, s, a, n_qwg);
   return launch_status("decode_prep_kernel");
 }
 
 static int launch_layer_prep(const DecodeArgs &a, const AppendArgs &ap, int64_t t_max,
                              hipStream_t s) {
   const int n_app = (a.B + kAppendRowsPerWg - 1) / kAppendRowsPerWg;
-  hipLaunchKernelGGL(decode_layer_prep_kernel, dim3(n_app + prep_workgroups(a, t_max)),
-                     dim3(kPrepThreads), 0, s, a, ap, a.B, n_app);
+  const int n_qwg = query_workgroups(a);
+  hipLaunchKernelGGL(decode_layer_prep_kernel, dim3(n_app + n_qwg + block_workgroups(t_max)),
+                     dim3(kPrepThreads), 0, s, a, ap, a.B, n_app, n_qwg);
   return launch_status("decode_layer_prep_kernel");
 }
 

@@ -233,3 +233,34 @@ def test_bad_block_id_is_flagged_not_faulted(gkv, cuda, torch_mod):
     bad, _ = allclose_report(res["out"][0], ref[0])
     assert bad == 0
     assert np.isfinite(res["out"]).all()
+
+
+def test_repeated_split_launches_reuse_the_plan(gkv, cuda, torch_mod):
+    """One prepare, then split + combine three times over the same workspace:
+    every repeat gives the same bits, within tolerance of the oracle."""
+    rng = np.random.default_rng(87)
+    L = lens_uniform(rng, 48, 100, 2000)
+    case = DecodeCase(48, 64, 8, L, window=0, scale=0.5, seed=88)
+    torch = torch_mod
+    dev = case.to_device(torch, cuda, *gkv.rope_table(case.cos.shape[0]))
+    view = gkv.cache_view(dev["k"], dev["v"], dev["table"], case.Hkv)
+    gkv.kv_append(dev["qkv"], case.Hq, dev["cos"], dev["sin"], dev["pos"], view,
+                  seq_lens=dev["seq_lens"], dev_err=dev["err"])
+    max_len = int(case.seq_lens.max())
+    ws = torch.empty(gkv.workspace_bytes(case.B, case.Hkv, max_len), dtype=torch.uint8,
+                     device=cuda)
+    kw = dict(cos_tab=dev["cos"], sin_tab=dev["sin"], workspace=ws, dev_err=dev["err"])
+    outs = []
+    for i in range(3):
+        out = torch.full((case.B, case.Hq * 64), float("nan"), dtype=torch.float32, device=cuda)
+        stages = ("prepare", "split", "combine") if i == 0 else ("split", "combine")
+        for st in stages:
+            gkv.decode_attention(dev["qkv"], dev["seq_lens"], max_len, view, dev["sinks"], out,
+                                 stage=st, **kw)
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy().reshape(case.B, case.Hq, 64))
+    assert int(dev["err"].item()) == 0
+    bad, worst = allclose_report(outs[0], case.oracle_out(), ATOL, RTOL)
+    assert bad == 0, f"{bad} outputs out of tolerance (max err {worst:.3e})"
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
