@@ -484,7 +484,8 @@ def main() -> int:
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
 
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"decode_split_config{args.config}_traffic.json")
+    vsfx = "_int8" if args.v_int8 else ""
+    tpath = os.path.join(ROOT, "profiles", f"decode_split_config{args.config}{vsfx}_traffic.json")
     if os.path.exists(tpath) and not args.split_tokens:
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
