@@ -245,7 +245,6 @@ def run_prefill(torch, gkv, args) -> int:
             view=view, window=view.ring,
             qkv=torch.randn(T, (Hq + 2 * Hkv) * D, generator=g, device=dev) * 0.5,
             sinks=torch.randn(Hq, generator=g, device=dev),
-            q=torch.empty(T, Hq * D, device=dev),
             k=torch.empty(T, Hkv * D, dtype=torch.bfloat16, device=dev),
             v=torch.empty(T, Hkv * D, dtype=torch.bfloat16, device=dev),
             out=torch.empty(T, Hq * D, dtype=torch.bfloat16, device=dev)))
@@ -265,13 +264,16 @@ def run_prefill(torch, gkv, args) -> int:
             e = [torch.cuda.Event(enable_timing=True) for _ in range(3)] if record else None
             if record:
                 e[0].record(stream)
+            # the append stores K/V (cache + packed rows); Q is rotated by the
+            # prefill as it loads the qkv rows
             gkv.kv_append(ly["qkv"], Hq, cos_d, sin_d, pos_d, ly["view"], row_seq=seq_d,
-                          seq_lens=lens_d, q_out=ly["q"], k_pack=ly["k"], v_pack=ly["v"],
-                          dev_err=err, stream=stream)
+                          seq_lens=lens_d, k_pack=ly["k"], v_pack=ly["v"], dev_err=err,
+                          stream=stream)
             if record:
                 e[1].record(stream)
-            gkv.prefill_attention(cu_d, max_len, ly["q"], ly["k"], ly["v"], ly["sinks"],
-                                  ly["out"], Hkv, window=ly["window"], stream=stream)
+            gkv.prefill_attention(cu_d, max_len, ly["qkv"], ly["k"], ly["v"], ly["sinks"],
+                                  ly["out"], Hkv, window=ly["window"], cos_tab=cos_d,
+                                  sin_tab=sin_d, stream=stream)
             if record:
                 e[2].record(stream)
                 ev.append((li, e))

@@ -210,14 +210,19 @@ int gkv_decode_layer_prepare(void *stream, int32_t B, int32_t n_q_heads, const f
 /* Causal attention of packed prompts with sinks: row j of prompt b (rows
  * cu_seqlens[b] .. cu_seqlens[b+1]-1, positions 0..L_b-1) attends to rows
  * 0..j of its prompt (window W: j-W+1..j):
- *   q        fp32 [rows][q_stride], rotated (gkv_kv_append's q_out)
+ *   q        fp32 [rows][q_stride]: rotated (gkv_kv_append's q_out) if cos_tab
+ *            is NULL; else not rotated (the qkv rows themselves, q_stride =
+ *            their row stride) and rotated on load at position j, bit-identical
+ *            to gkv_kv_append's q_out
+ *   cos_tab/sin_tab  NULL (both), or device copies of gkv_rope_table rows
  *   k, v     bf16 [rows][Hkv][64] (gkv_kv_append's k_pack, v_pack)
  *   cu_seqlens device int32 [B+1]; max_len = host bound of the prompt lengths
  *   out      [rows][out_stride] of out_dtype */
 int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_seqlens, int32_t max_len,
                           int32_t n_q_heads, int32_t n_kv_heads, const float *q,
-                          int64_t q_stride, const void *k, const void *v, const float *sinks,
-                          int32_t window, void *out, int64_t out_stride, int32_t out_dtype);
+                          int64_t q_stride, const float *cos_tab, const float *sin_tab,
+                          const void *k, const void *v, const float *sinks, int32_t window,
+                          void *out, int64_t out_stride, int32_t out_dtype);
 
 /* ---- Paged KV pool (host bookkeeping, device storage) -------------------- */
 

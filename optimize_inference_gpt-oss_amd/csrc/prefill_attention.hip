@@ -44,6 +44,7 @@ struct PrefillArgs {
   const int32_t *cu;
   const float *q;
   int64_t q_stride;
+  const float *cos_tab, *sin_tab; // nullptr: q is rotated; else rotate row j at position j
   const uint16_t *k, *v;
   int64_t kv_stride; // elements per packed row: Hkv * 64
   const float *sinks;
@@ -117,13 +118,30 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
     const float qscale = 0.125f * kLog2e; // 1/sqrt(64); exp -> exp2
 #pragma unroll
     for (int c = 0; c < 2; c++) {
-      const int row = row0 + min(q0 + 16 * c + n, L - 1);
-      const float *qp = a.q + (int64_t)row * a.q_stride + h * D + 8 * kg;
+      const int pos = min(q0 + 16 * c + n, L - 1);
+      const float *qp = a.q + (int64_t)(row0 + pos) * a.q_stride + h * D + 8 * kg;
+      // the two halves of RoPE pairs 8kg .. 8kg+7 sit in this lane
+      float qv[2][8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        qv[0][j] = qp[j];
+        qv[1][j] = qp[32 + j];
+      }
+      if (a.cos_tab) {
+        const float *cp = a.cos_tab + (int64_t)pos * (D / 2) + 8 * kg;
+        const float *sp = a.sin_tab + (int64_t)pos * (D / 2) + 8 * kg;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const float x1 = qv[0][j], x2 = qv[1][j], cs = cp[j], sn = sp[j];
+          qv[0][j] = rope_first(x1, x2, cs, sn);
+          qv[1][j] = rope_second(x1, x2, cs, sn);
+        }
+      }
 #pragma unroll
       for (int dh = 0; dh < 2; dh++) {
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-          const float x = qp[32 * dh + j] * qscale;
+          const float x = qv[dh][j] * qscale;
           const __bf16 hi = (__bf16)x;
           qhi[c][dh][j] = hi;
           qlo[c][dh][j] = (__bf16)(x - (float)hi);
@@ -267,8 +285,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
 
 extern "C" int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_seqlens,
                                      int32_t max_len, int32_t n_q_heads, int32_t n_kv_heads,
-                                     const float *q, int64_t q_stride, const void *k,
-                                     const void *v, const float *sinks, int32_t window, void *out,
+                                     const float *q, int64_t q_stride, const float *cos_tab,
+                                     const float *sin_tab, const void *k, const void *v,
+                                     const float *sinks, int32_t window, void *out,
                                      int64_t out_stride, int32_t out_dtype) {
   using namespace gkv;
   if (B < 0 || max_len < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || window < 0 ||
@@ -276,7 +295,7 @@ extern "C" int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_
     return GKV_ERR_ARG;
   if (B > 0 && (!cu_seqlens || !q || !k || !v || !sinks || !out))
     return GKV_ERR_ARG;
-  if (n_q_heads % n_kv_heads != 0)
+  if (n_q_heads % n_kv_heads != 0 || (cos_tab == nullptr) != (sin_tab == nullptr))
     return GKV_ERR_ARG;
   const int G = n_q_heads / n_kv_heads;
   if (G > 8)
@@ -296,6 +315,8 @@ extern "C" int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_
   a.cu = cu_seqlens;
   a.q = q;
   a.q_stride = q_stride;
+  a.cos_tab = cos_tab;
+  a.sin_tab = sin_tab;
   a.k = (const uint16_t *)k;
   a.v = (const uint16_t *)v;
   a.kv_stride = (int64_t)n_kv_heads * kHeadDim;

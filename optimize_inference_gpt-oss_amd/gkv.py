@@ -101,7 +101,7 @@ SIGNATURES = {
     "gkv_decode_combine": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _i32, _i32, _vp, _i32,
                                           _vp, _sz, _vp, _i64, _i32]),
     "gkv_prefill_attention": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i32, _i32, _vp, _i64, _vp,
-                                             _vp, _vp, _i32, _vp, _i64, _i32]),
+                                             _vp, _vp, _vp, _vp, _i32, _vp, _i64, _i32]),
     "gkv_pool_create": (ctypes.c_int, [ctypes.POINTER(PoolConfig), ctypes.POINTER(_vp)]),
     "gkv_pool_destroy": (ctypes.c_int, [_vp]),
     "gkv_pool_seq_alloc": (ctypes.c_int, [_vp, ctypes.POINTER(_i32)]),
@@ -261,13 +261,15 @@ def decode_layer(qkv, seq_lens, max_seq_len, view: CacheView, sinks, out, cos_ta
 
 
 def prefill_attention(cu_seqlens, max_len, q, k, v, sinks, out, n_kv_heads, window=0,
-                      stream=None):
+                      cos_tab=None, sin_tab=None, stream=None):
+    """q: rotated rows, or (with cos_tab/sin_tab) the raw qkv rows, rotated on load."""
     import torch
     out_dtype = BF16 if out.dtype == torch.bfloat16 else F32
     st = lib().gkv_prefill_attention(stream_handle(stream), cu_seqlens.shape[0] - 1,
                                      ptr(cu_seqlens), max_len, sinks.shape[0], n_kv_heads,
-                                     ptr(q), q.stride(0), ptr(k), ptr(v), ptr(sinks), window,
-                                     ptr(out), out.stride(0), out_dtype)
+                                     ptr(q), q.stride(0), ptr(cos_tab), ptr(sin_tab), ptr(k),
+                                     ptr(v), ptr(sinks), window, ptr(out), out.stride(0),
+                                     out_dtype)
     check("gkv_prefill_attention", st)
 
 

@@ -79,7 +79,9 @@ class PrefillCase:
                                    O.from_bf16(self.vb), self.sinks, window=self.window)
 
 
-def run_gpu(case, gkv, torch, dev, out_dtype=None, ring=True):
+def run_gpu(case, gkv, torch, dev, out_dtype=None, ring=True, rotate_in_prefill=False):
+    """rotate_in_prefill: the append writes no rotated Q; the prefill reads
+    the qkv rows and rotates Q on load."""
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
     qkv = t(case.qkv)
     cos, sin = gkv.rope_table(max(case.max_len, 1))
@@ -98,12 +100,18 @@ def run_gpu(case, gkv, torch, dev, out_dtype=None, ring=True):
     v_pack = torch.zeros((T, case.Hkv * D), dtype=torch.int16, device=dev)
     err = torch.zeros(1, dtype=torch.int32, device=dev)
     lens = t(case.L.astype(np.int32))
-    gkv.kv_append(qkv, case.Hq, t(cos), t(sin), t(case.pos), view, row_seq=t(case.row_seq),
-                  seq_lens=lens, q_out=q_out, k_pack=k_pack, v_pack=v_pack, dev_err=err)
+    cos_d, sin_d = t(cos), t(sin)
+    gkv.kv_append(qkv, case.Hq, cos_d, sin_d, t(case.pos), view, row_seq=t(case.row_seq),
+                  seq_lens=lens, q_out=None if rotate_in_prefill else q_out, k_pack=k_pack,
+                  v_pack=v_pack, dev_err=err)
     out = torch.full((T, case.Hq * D), float("nan"), dtype=out_dtype or torch.float32,
                      device=dev)
-    gkv.prefill_attention(t(case.cu), case.max_len, q_out, k_pack, v_pack, t(case.sinks), out,
-                          case.Hkv, window=case.window)
+    if rotate_in_prefill:
+        gkv.prefill_attention(t(case.cu), case.max_len, qkv, k_pack, v_pack, t(case.sinks), out,
+                              case.Hkv, window=case.window, cos_tab=cos_d, sin_tab=sin_d)
+    else:
+        gkv.prefill_attention(t(case.cu), case.max_len, q_out, k_pack, v_pack, t(case.sinks),
+                              out, case.Hkv, window=case.window)
     torch.cuda.synchronize()
     return dict(
         err=int(err.item()),
@@ -175,6 +183,18 @@ def test_prompt_append_into_int8_v_cache(oracle, gkv, cuda, window):
     case = PrefillCase(oracle, 90 + window, [1, 16, 130, 300], 64, 8, window=window,
                        v_int8=True)
     check(case, run_gpu(case, gkv, torch, cuda))
+
+
+@pytest.mark.parametrize("window", [0, 128])
+def test_rotate_on_load_matches_rotated_q(oracle, gkv, cuda, window):
+    """The prefill rotating Q from the raw qkv rows gives the same output bits
+    as the prefill on the append's rotated Q (and matches the oracle)."""
+    import torch
+    case = PrefillCase(oracle, 95 + window, [1, 33, 130, 300, 517], 64, 8, window=window)
+    a = run_gpu(case, gkv, torch, cuda)
+    b = run_gpu(case, gkv, torch, cuda, rotate_in_prefill=True)
+    check(case, a)
+    assert np.array_equal(a["out"].view(np.uint32), b["out"].view(np.uint32))
 
 
 def test_empty_batch_and_zero_length(oracle, gkv, cuda):
