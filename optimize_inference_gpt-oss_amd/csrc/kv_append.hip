@@ -12,14 +12,20 @@
 // Layout written: 2 KB per block and head for K and for V, in the orders of
 // k_offset / v_offset (kv_append.hpp), which put each lane's matrix-core
 // operand pieces of the attention kernel in 16 contiguous bytes, in lane
-// order. One workgroup per row; HBM-bound and tiny
+// order. 256 threads per row, 4 rows per workgroup (a prompt's append has
+// tens of thousands of rows: fewer, larger workgroups launch faster); HBM-bound
 // (2 KB written per token per layer).
 #include "kv_append.hpp"
 
 namespace gkv {
 
-__global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
-  append_row(a, blockIdx.x, threadIdx.x, blockDim.x);
+constexpr int kRowThreads = 256, kRowsPerWg = 4;
+
+__global__ __launch_bounds__(kRowThreads *kRowsPerWg) void kv_append_kernel(AppendArgs a,
+                                                                           int n_rows) {
+  const int r = blockIdx.x * kRowsPerWg + threadIdx.x / kRowThreads;
+  if (r < n_rows)
+    append_row(a, r, threadIdx.x % kRowThreads, kRowThreads);
 }
 
 } // namespace gkv
@@ -74,6 +80,7 @@ extern "C" int gkv_kv_append(void *stream, int32_t n_rows, const float *qkv, int
   a.dev_err = dev_err;
   a.v_int8 = cache.v_format == GKV_V_INT8;
   a.vs = (float *)cache.v_scale;
-  hipLaunchKernelGGL(kv_append_kernel, dim3(n_rows), dim3(256), 0, (hipStream_t)stream, a);
+  hipLaunchKernelGGL(kv_append_kernel, dim3((n_rows + kRowsPerWg - 1) / kRowsPerWg),
+                     dim3(kRowThreads * kRowsPerWg), 0, (hipStream_t)stream, a, n_rows);
   return launch_status(__func__);
 }
