@@ -588,12 +588,14 @@ void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
     for (int i = 1; i < 8; i++)
       mx = fmaxf(mx, sc[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
     // Lazy rescale: the reference max moves only when a score exceeds it by
     // more than 8 (weights stay below 2^8, harmless in fp32); the final
-    // normalisation uses the same max, so the result does not change.
+    // normalisation uses the same max, so the result does not change. The
+    // test needs no cross-lane max (m_run is the same in the 4 lanes of a
+    // column); only the rescale does.
     if (__any(mx > m_run + 8.0f)) {
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run, mx);
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       m_run = m_new;

@@ -1,5 +1,5 @@
 // Causal attention of a packed batch of prompts with per-head sinks and the
-// sliding window, on bf16 matrix cores.
+// sliding window, on bf16 and fp16 matrix cores.
 //
 // The reference has no prefill kernel: it feeds a prompt one token at a time
 // through the decode step (getp-csrc/engine/gpu_engine.hpp:811-813), so each
@@ -18,9 +18,10 @@
 //   scores  S^T[key][query] = K[key][dims] * Q^T[dims][query]; the query is
 //           carried as bf16 high + low pieces accumulated into one tile, so
 //           the scores keep ~16 mantissa bits of the fp32 query
-//   output  O^T[dim][query] += V^T[dim][keys] * P^T[keys][query], P again as
-//           bf16 high + low pieces (a single bf16 P leaves errors of 2^-9 of
-//           |v| on queries that see few keys)
+//   output  O^T[dim][query] += V^T[dim][keys] * P^T[keys][query] on
+//           v_mfma_f32_16x16x32_f16: P (in [0, 1]) as one fp16 piece, V as fp16
+//           of v * 2^-10 (a single bf16 P leaves errors of 2^-9 of |v| on
+//           queries that see few keys; fp16 keeps 2^-12)
 //   A 32-key step uses two 16-key score tiles; lane (kg, n) holds keys
 //   4kg..4kg+3 of each, which are its P^T operand slots; the V^T operand is
 //   the same 8 keys of one dim, read from V stored transposed in LDS.
@@ -28,8 +29,8 @@
 // rescale by threshold 8, the running max seeded with the sink, and the sink
 // added in the final normalisation, as in the decode kernel.
 //
-// LDS: K tile [64 keys][64 dims + 8 pad], V^T tile [64 dims][64 keys + 8 pad],
-// double-buffered (36 KB); tile t + 1 is fetched into registers while tile t
+// LDS: K tile [64 keys][64 dims + 8 pad] bf16, V^T tile [64 dims][64 keys + 8 pad]
+// fp16, double-buffered (36 KB); tile t + 1 is fetched into registers while tile t
 // is consumed.
 #include "gkv_device.hpp"
 
@@ -38,7 +39,9 @@ namespace gkv {
 constexpr int kQBlock = 32;         // query positions per workgroup
 constexpr int kKTile = 64;          // keys per LDS tile
 constexpr int kKRow = kHeadDim + 8; // bf16 per K row in LDS (pad against bank conflicts)
-constexpr int kVRow = kKTile + 8;   // bf16 per V^T row in LDS
+constexpr int kVRow = kKTile + 8;   // fp16 per V^T row in LDS
+constexpr float kVScale = 0x1p-10f; // V is staged as fp16 of v * kVScale
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 struct PrefillArgs {
   const int32_t *cu;
@@ -85,8 +88,14 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   const bool active = wave < a.G;
   const int h = g * a.G + (active ? wave : 0);
 
-  // ---- K/V tile staging: thread piece i covers key (tid + i*NT) / 8, dims 8 * ((tid + i*NT) % 8)
-  u32x4 kreg[kLoads], vreg[kLoads];
+  // ---- K/V tile staging.
+  // K: piece i of a thread covers key (tid + i*NT) / 8, dims 8 * ((tid + i*NT) % 8).
+  // V: piece i covers keys 2pr, 2pr + 1 and dims 4pd .. 4pd+3, where virtual
+  // wave vw = (tid + i*NT) / 64 and its lane ln give pr = ln % 16 + 16 (vw % 2),
+  // pd = ln / 16 + 4 (vw / 2); the pair is stored as one dword per dim of V^T,
+  // and the 64 dwords a wave writes fall in 64 different banks.
+  u32x4 kreg[kLoads];
+  u32x2 va[kLoads], vb[kLoads];
   auto fetch = [&](int t) {
     const int kt0 = k_lo + t * kKTile;
 #pragma unroll
@@ -94,10 +103,20 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
       const int idx = tid + i * NT;
       const int key = idx >> 3, part = idx & 7;
       const int row = row0 + min(kt0 + key, L - 1); // clamped: rows past the prompt are masked
-      const int64_t off = (int64_t)row * a.kv_stride + g * D + part * 8;
-      kreg[i] = *(const u32x4 *)(a.k + off);
-      vreg[i] = *(const u32x4 *)(a.v + off);
+      kreg[i] = *(const u32x4 *)(a.k + (int64_t)row * a.kv_stride + g * D + part * 8);
+      const int vw = idx >> 6, ln = idx & 63;
+      const int pr = (ln & 15) + 16 * (vw & 1), pd = (ln >> 4) + 4 * (vw >> 1);
+      const int ra = row0 + min(kt0 + 2 * pr, L - 1), rb = row0 + min(kt0 + 2 * pr + 1, L - 1);
+      va[i] = *(const u32x2 *)(a.v + (int64_t)ra * a.kv_stride + g * D + pd * 4);
+      vb[i] = *(const u32x2 *)(a.v + (int64_t)rb * a.kv_stride + g * D + pd * 4);
     }
+  };
+  // V goes to LDS as fp16 of v * 2^-10: exact for bf16 magnitudes 2^-4 .. 2^26,
+  // an absolute error of at most 2^-15 below that (fp16 subnormals), inf above
+  // (so the output shows it). P then enters the matrix core as one fp16 piece.
+  auto v_half = [](uint32_t bits16) -> uint32_t {
+    const _Float16 h = (_Float16)(bf16_to_f32((uint16_t)bits16) * kVScale);
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
   };
   auto stash = [&](int buf) {
 #pragma unroll
@@ -105,10 +124,14 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
       const int idx = tid + i * NT;
       const int key = idx >> 3, part = idx & 7;
       *(u32x4 *)&k_lds[buf][key * kKRow + part * 8] = kreg[i];
-      const uint16_t *vv = (const uint16_t *)&vreg[i];
+      const int vw = idx >> 6, ln = idx & 63;
+      const int pr = (ln & 15) + 16 * (vw & 1), pd = (ln >> 4) + 4 * (vw >> 1);
 #pragma unroll
-      for (int j = 0; j < 8; j++)
-        v_lds[buf][(part * 8 + j) * kVRow + key] = vv[j];
+      for (int j = 0; j < 4; j++) {
+        const uint32_t wa = va[i][j >> 1] >> (16 * (j & 1)), wb = vb[i][j >> 1] >> (16 * (j & 1));
+        *(uint32_t *)&v_lds[buf][(4 * pd + j) * kVRow + 2 * pr] =
+            v_half(wa & 0xffffu) | (v_half(wb & 0xffffu) << 16);
+      }
     }
   };
 
@@ -189,7 +212,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
           }
         }
       }
-      bf16x8 phi[2], plo[2];
+      f16x8 ph[2];
 #pragma unroll
       for (int c = 0; c < 2; c++) {
         float sc[8];
@@ -213,10 +236,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
 #pragma unroll
         for (int i = 1; i < 8; i++)
           mx = fmaxf(mx, sc[i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        // lazy rescale: the reference max moves only when exceeded by more than 8
+        // lazy rescale: the reference max moves only when exceeded by more than 8;
+        // the test needs no cross-lane max (m_run is the same in the 4 lanes of
+        // a column), only the rescale does
         if (__any(mx > m_run[c] + 8.0f)) {
+          mx = fmaxf(mx, __shfl_xor(mx, 16));
+          mx = fmaxf(mx, __shfl_xor(mx, 32));
           const float m_new = fmaxf(m_run[c], mx);
           const float alpha = __builtin_amdgcn_exp2f(m_run[c] - m_new);
           m_run[c] = m_new;
@@ -229,9 +254,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
         for (int i = 0; i < 8; i++) {
           const float p = __builtin_amdgcn_exp2f(sc[i] - m_run[c]);
           lsum[c] += p;
-          const __bf16 hi = (__bf16)p;
-          phi[c][i] = hi;
-          plo[c][i] = (__bf16)(p - (float)hi);
+          ph[c][i] = (_Float16)p;
         }
       }
 #pragma unroll
@@ -239,12 +262,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
         const uint16_t *vrow = &v_lds[buf][(16 * nn + n) * kVRow + 32 * s + 4 * kg];
         const u32x2 x = *(const u32x2 *)vrow;
         const u32x2 y = *(const u32x2 *)(vrow + 16);
-        const bf16x8 vop = __builtin_bit_cast(bf16x8, u32x4{x[0], x[1], y[0], y[1]});
+        const f16x8 vop = __builtin_bit_cast(f16x8, u32x4{x[0], x[1], y[0], y[1]});
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
-          o[c][nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, phi[c], o[c][nn], 0, 0, 0);
-          o[c][nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, plo[c], o[c][nn], 0, 0, 0);
-        }
+        for (int c = 0; c < 2; c++)
+          o[c][nn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, ph[c], o[c][nn], 0, 0, 0);
       }
     }
     if (t + 1 < n_tiles)
@@ -265,7 +286,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
       continue;
     const float M2 = fmaxf(m_run[c], sink2);
     const float f = __builtin_amdgcn_exp2f(m_run[c] - M2);
-    const float scale = f / fmaf(ls, f, __builtin_amdgcn_exp2f(sink2 - M2));
+    const float scale = f / fmaf(ls, f, __builtin_amdgcn_exp2f(sink2 - M2)) / kVScale;
     const int64_t ob = (int64_t)(row0 + qa) * a.out_stride + (int64_t)h * D + 4 * kg;
 #pragma unroll
     for (int nn = 0; nn < 4; nn++) {
