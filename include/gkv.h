@@ -123,7 +123,9 @@ int gkv_rope_table(const gkv_rope_config *cfg, int32_t n_pos, float *cos_tab, fl
  *   k_pack/v_pack NULL, or bf16 [rows][Hkv][64] receiving the same bf16 K, V
  *                (the packed operands of gkv_prefill_attention)
  *   dev_err      NULL, or a device uint32 that gets GKV_DEVERR_* bits
- * cos_tab/sin_tab: device copies of gkv_rope_table rows. */
+ * cos_tab/sin_tab: device copies of gkv_rope_table rows. qkv, the tables and
+ * the packed rows are 16-byte aligned and row_stride is a multiple of 4
+ * (GKV_ERR_ARG otherwise). */
 int gkv_kv_append(void *stream, int32_t n_rows, const float *qkv, int64_t row_stride,
                   int32_t n_q_heads, const float *cos_tab, const float *sin_tab,
                   const int32_t *row_pos, const int32_t *row_seq, const int32_t *seq_lens,

@@ -315,11 +315,12 @@ __global__ __launch_bounds__(kPrepThreads) void decode_prep_kernel(DecodeArgs a,
 
 // The append of a decode layer (row b = the new token of sequence b, at
 // position seq_lens[b] - 1) and the prepare work in one launch: workgroups
-// 0 .. n_app-1 append 4 rows each (256 threads per row), the next n_qwg
+// 0 .. n_app-1 append 4 rows each (4 waves per row), the next n_qwg
 // prepare the query operands, the others the plan and the stream blocks. The
 // parts touch disjoint memory (the prepare reads the raw query of the qkv
 // rows, the block tables and the lengths).
-constexpr int kAppendRowsPerWg = kPrepThreads / 256;
+constexpr int kAppendWavesPerRow = 4; // one kv-head pair per wave at Hkv = 8
+constexpr int kAppendRowsPerWg = kPrepThreads / 64 / kAppendWavesPerRow;
 __global__ __launch_bounds__(kPrepThreads) void decode_layer_prep_kernel(DecodeArgs a,
                                                                          AppendArgs ap,
                                                                          int n_rows,
@@ -327,9 +328,10 @@ __global__ __launch_bounds__(kPrepThreads) void decode_layer_prep_kernel(DecodeA
                                                                          int n_qwg) {
   const int wg = blockIdx.x;
   if (wg < n_app) {
-    const int r = wg * kAppendRowsPerWg + (threadIdx.x >> 8);
+    const int wave = threadIdx.x >> 6;
+    const int r = wg * kAppendRowsPerWg + wave / kAppendWavesPerRow;
     if (r < n_rows)
-      append_row(ap, r, threadIdx.x & 255, 256);
+      append_row(ap, r, threadIdx.x & 63, wave % kAppendWavesPerRow, kAppendWavesPerRow);
   } else if (wg < n_app + n_qwg) {
     prep_query_items(a, wg - n_app, n_qwg);
   } else {
@@ -1014,6 +1016,8 @@ static int layer_append_args(AppendArgs &ap, int32_t B, int32_t n_q_heads, const
     return GKV_ERR_ARG;
   if (row_stride < (int64_t)(n_q_heads + 2 * cache.n_kv_heads) * kHeadDim)
     return GKV_ERR_ARG;
+  if (row_stride % 4 != 0 || ((uintptr_t)qkv | (uintptr_t)cos_tab | (uintptr_t)sin_tab) % 16 != 0)
+    return GKV_ERR_ARG; // 16-byte vector loads in the append
   if (cache.ring % kBlockTokens != 0)
     return GKV_ERR_UNSUPPORTED;
   ap.qkv = qkv;

@@ -12,20 +12,73 @@
 // Layout written: 2 KB per block and head for K and for V, in the orders of
 // k_offset / v_offset (kv_append.hpp), which put each lane's matrix-core
 // operand pieces of the attention kernel in 16 contiguous bytes, in lane
-// order. 256 threads per row, 4 rows per workgroup (a prompt's append has
-// tens of thousands of rows: fewer, larger workgroups launch faster); HBM-bound
-// (2 KB written per token per layer).
+// order. One wave per row, 16 rows per workgroup: a row's chain of dependent
+// loads (its sequence, length and block id) is short work for one wave, and a
+// prompt's tens of thousands of rows keep many chains in flight. HBM-bound
+// (4 KB of K/V read and 2 KB written per token per layer, twice that with the
+// packed rows).
 #include "kv_append.hpp"
 
 namespace gkv {
 
-constexpr int kRowThreads = 256, kRowsPerWg = 4;
+constexpr int kRowsPerWg = 16;
+constexpr int kMaxStageHeads = 8; // bf16 V rows staged in LDS up to this many kv heads
 
-__global__ __launch_bounds__(kRowThreads *kRowsPerWg) void kv_append_kernel(AppendArgs a,
-                                                                           int n_rows) {
-  const int r = blockIdx.x * kRowsPerWg + threadIdx.x / kRowThreads;
+// With a bf16 V cache the rows' V goes through LDS: four rows of the
+// workgroup holding slots 4m .. 4m+3 of one block (consecutive tokens of a
+// prompt) are written together, as 16-byte pieces (dims d and d+16 of the 4
+// tokens, contiguous in the V block layout), which fill whole 128-byte lines;
+// storing one token's values alone scatters 2-byte writes over the block and
+// leaves partly written lines. Rows without such a quad store element-wise.
+__global__ __launch_bounds__(64 * kRowsPerWg) void kv_append_kernel(AppendArgs a, int n_rows) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[kRowsPerWg][kMaxStageHeads * kHeadDim];
+  __shared__ int s_slot[kRowsPerWg], s_seq[kRowsPerWg];
+  __shared__ int64_t s_base[kRowsPerWg];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r = blockIdx.x * kRowsPerWg + w;
+  const bool staged = !a.v_int8 && a.vc && a.n_kv_heads <= kMaxStageHeads;
+  RowPlace pl{0, -1, -1, 0};
   if (r < n_rows)
-    append_row(a, r, threadIdx.x % kRowThreads, kRowThreads);
+    pl = append_row(a, r, lane, 0, 1, staged ? s_v[w] : nullptr);
+  if (!staged)
+    return;
+  if (lane == 0) {
+    s_slot[w] = pl.store ? pl.slot : -1;
+    s_seq[w] = pl.seq;
+    s_base[w] = pl.base;
+  }
+  __syncthreads();
+  auto leads = [&](int i) {
+    if (i < 0 || i + 3 >= kRowsPerWg || s_slot[i] < 0 || (s_slot[i] & 3) != 0)
+      return false;
+    for (int k = 1; k < 4; k++)
+      if (s_slot[i + k] != s_slot[i] + k || s_seq[i + k] != s_seq[i] ||
+          s_base[i + k] != s_base[i])
+        return false;
+    return true;
+  };
+  const bool in_quad = leads(w) || leads(w - 1) || leads(w - 2) || leads(w - 3);
+  constexpr int D = kHeadDim;
+  if (pl.store && !in_quad) {
+    const int off = pl.slot % kBlockTokens;
+    for (int idx = lane; idx < a.n_kv_heads * D; idx += 64) {
+      const int g = idx / D, d = idx % D;
+      a.vc[pl.base + (int64_t)g * (kBlockTokens * D) + v_offset(off, d)] = s_v[w][idx];
+    }
+  }
+  if (leads(w)) {
+    const int t0 = pl.slot % kBlockTokens; // 4m
+    for (int p = lane; p < a.n_kv_heads * 32; p += 64) {
+      const int g = p / 32, d = 32 * ((p / 16) % 2) + p % 16; // dims d and d + 16
+      uint16_t h[8];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        h[k] = s_v[w + k][g * D + d];
+        h[4 + k] = s_v[w + k][g * D + d + 16];
+      }
+      *(u32x4 *)(a.vc + pl.base + (int64_t)g * (kBlockTokens * D) + v_offset(t0, d)) = pack8(h);
+    }
+  }
 }
 
 } // namespace gkv
@@ -44,6 +97,11 @@ extern "C" int gkv_kv_append(void *stream, int32_t n_rows, const float *qkv, int
     return GKV_ERR_ARG;
   const int64_t qkv_width = (int64_t)(n_q_heads + 2 * cache.n_kv_heads) * kHeadDim;
   if (row_stride < qkv_width || (q_out && q_out_stride < (int64_t)n_q_heads * kHeadDim))
+    return GKV_ERR_ARG;
+  // 16-byte vector loads and stores
+  if (row_stride % 4 != 0 ||
+      ((uintptr_t)qkv | (uintptr_t)cos_tab | (uintptr_t)sin_tab | (uintptr_t)k_pack |
+       (uintptr_t)v_pack) % 16 != 0)
     return GKV_ERR_ARG;
   const bool to_cache = cache.k != nullptr || cache.v != nullptr;
   if (to_cache && (!cache.k || !cache.v || !cache.block_table || cache.table_stride <= 0 ||
@@ -81,6 +139,6 @@ extern "C" int gkv_kv_append(void *stream, int32_t n_rows, const float *qkv, int
   a.v_int8 = cache.v_format == GKV_V_INT8;
   a.vs = (float *)cache.v_scale;
   hipLaunchKernelGGL(kv_append_kernel, dim3((n_rows + kRowsPerWg - 1) / kRowsPerWg),
-                     dim3(kRowThreads * kRowsPerWg), 0, (hipStream_t)stream, a, n_rows);
+                     dim3(64 * kRowsPerWg), 0, (hipStream_t)stream, a, n_rows);
   return launch_status(__func__);
 }

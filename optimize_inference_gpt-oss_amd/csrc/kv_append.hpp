@@ -45,8 +45,33 @@ __host__ __device__ __forceinline__ int v_int8_offset(int d, int t) {
   return ((d % 16) * 4 + t / 4) * 16 + (d / 16) * 4 + t % 4;
 }
 
-// Row r of the call, by nt threads numbered tid = 0 .. nt-1.
-__device__ __forceinline__ void append_row(const AppendArgs &a, int r, int tid, int nt) {
+// Eight bf16 (bits) as one 16-byte piece, element 0 first.
+__device__ __forceinline__ u32x4 pack8(const uint16_t *h) {
+  return u32x4{h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+               h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16)};
+}
+
+// Row r of the call, by one wave (lane = 0..63). Lanes 0-31 take the keys:
+// lane (g, j) of head g = lane / 4 rotates the pairs (8j + i, 32 + 8j + i),
+// i = 0..7, and stores dims 8j..8j+7 and 32+8j..32+8j+7 as two 16-byte pieces
+// (contiguous in the K block layout and in the packed row). The qkv rows,
+// tables and packed rows are 16-byte aligned (checked by the callers). Lanes 32-63 take the values:
+// dims 16q .. 16q+15 of head g, with (g, q) = ((lane - 32) / 4, lane % 4).
+// More kv heads than 8 loop.
+// Where a row's token went: its sequence, its slot and the element offset of
+// its block in the pool (store = 0: not stored).
+struct RowPlace {
+  int store, seq, slot;
+  int64_t base;
+};
+
+// part / n_parts: the row may be shared by n_parts waves, wave `part` taking
+// every n_parts-th kv head (and query pair); a head's 4 key and 4 value lanes
+// stay adjacent in one wave (the int8 scale is their max). v_stage: NULL, or bf16 [Hkv * 64] in LDS that receives the
+// row's V; then the bf16 V cache store is left to the caller.
+__device__ __forceinline__ RowPlace append_row(const AppendArgs &a, int r, int lane,
+                                               int part = 0, int n_parts = 1,
+                                               uint16_t *v_stage = nullptr) {
   constexpr int D = kHeadDim, HALF = kHeadDim / 2;
   const int seq = a.row_seq ? a.row_seq[r] : r;
   // the row's position: given, or the last position of its sequence
@@ -55,10 +80,10 @@ __device__ __forceinline__ void append_row(const AppendArgs &a, int r, int tid, 
   const float *cs = a.cos_tab + (int64_t)pos * HALF, *sn = a.sin_tab + (int64_t)pos * HALF;
   const int kv_dim = a.n_kv_heads * D;
 
-  // Rotated query (each thread owns whole pairs, so q_out may alias qkv).
+  // Rotated query (each lane owns whole pairs, so q_out may alias qkv).
   if (a.q_out) {
     float *qo = a.q_out + (int64_t)r * a.q_out_stride;
-    for (int idx = tid; idx < a.n_q_heads * HALF; idx += nt) {
+    for (int idx = part * 64 + lane; idx < a.n_q_heads * HALF; idx += 64 * n_parts) {
       const int h = idx / HALF, i = idx % HALF;
       const float x1 = row[h * D + i], x2 = row[h * D + HALF + i];
       const float c = cs[i], s = sn[i];
@@ -78,13 +103,13 @@ __device__ __forceinline__ void append_row(const AppendArgs &a, int r, int tid, 
   if (store) {
     const int blk = slot / kBlockTokens;
     if (blk >= a.table_stride) {
-      if (tid == 0 && a.dev_err)
+      if (lane == 0 && part == 0 && a.dev_err)
         atomicOr(a.dev_err, GKV_DEVERR_LENGTH);
       store = false;
     } else {
       const int phys = a.table[(int64_t)seq * a.table_stride + blk];
       if (phys < 0 || phys >= a.num_blocks) {
-        if (tid == 0 && a.dev_err)
+        if (lane == 0 && part == 0 && a.dev_err)
           atomicOr(a.dev_err, GKV_DEVERR_BLOCK_ID);
         store = false;
       } else {
@@ -94,56 +119,84 @@ __device__ __forceinline__ void append_row(const AppendArgs &a, int r, int tid, 
     }
   }
 
+  const RowPlace place{store ? 1 : 0, seq, slot, kbase};
   const float *kr = row + a.n_q_heads * D, *vr = kr + kv_dim;
-  for (int idx = tid; idx < a.n_kv_heads * HALF; idx += nt) {
-    const int g = idx / HALF, i = idx % HALF;
-    const float x1 = kr[g * D + i], x2 = kr[g * D + HALF + i];
-    const float c = cs[i], s = sn[i];
-    const uint16_t k1 = f32_to_bf16_rne(rope_first(x1, x2, c, s));
-    const uint16_t k2 = f32_to_bf16_rne(rope_second(x1, x2, c, s));
-    if (store) {
-      uint16_t *kd = a.kc + kbase + (int64_t)g * (kBlockTokens * D);
-      kd[k_offset(off, i)] = k1;
-      kd[k_offset(off, HALF + i)] = k2;
-    }
-    if (a.k_pack) {
-      uint16_t *kp = a.k_pack + (int64_t)r * kv_dim + g * D;
-      kp[i] = k1;
-      kp[HALF + i] = k2;
-    }
-  }
-  if (a.v_int8) {
-    // One wave per head (nt and kv_dim are multiples of 64): the head's
-    // max |v| across the wave, then the reference's rule,
-    // getp-csrc/kernels/fast_misc.hpp:74-84.
-    for (int idx = tid; idx < kv_dim; idx += nt) {
-      const int g = idx / D, d = idx % D;
-      const float x = vr[idx];
-      float amax = fabsf(x);
+  if (lane < 32) {
+    for (int g = (lane / 4) * n_parts + part; g < a.n_kv_heads; g += 8 * n_parts) {
+      const int j = lane % 4;
+      const f32x4 *k1p = (const f32x4 *)(kr + g * D + 8 * j);
+      const f32x4 *k2p = (const f32x4 *)(kr + g * D + HALF + 8 * j);
+      const f32x4 *cp = (const f32x4 *)(cs + 8 * j), *sp = (const f32x4 *)(sn + 8 * j);
+      const f32x4 x1[2] = {k1p[0], k1p[1]}, x2[2] = {k2p[0], k2p[1]};
+      const f32x4 c[2] = {cp[0], cp[1]}, s[2] = {sp[0], sp[1]};
+      uint16_t o1[8], o2[8];
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1)
-        amax = fmaxf(amax, __shfl_xor(amax, o));
-      const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
-      const float c = fminf(fmaxf(rintf(x * inv), -127.0f), 127.0f);
-      if (store) {
-        int8_t *vq = (int8_t *)a.vc + vbase + (int64_t)g * (kBlockTokens * D);
-        vq[v_int8_offset(d, off)] = (int8_t)c;
-        if (d == 0)
-          a.vs[vbase / D + (int64_t)g * kBlockTokens + off] = amax / 127.0f;
+      for (int i = 0; i < 8; i++) {
+        const float a1 = x1[i / 4][i % 4], a2 = x2[i / 4][i % 4];
+        const float cc = c[i / 4][i % 4], ss = s[i / 4][i % 4];
+        o1[i] = f32_to_bf16_rne(rope_first(a1, a2, cc, ss));
+        o2[i] = f32_to_bf16_rne(rope_second(a1, a2, cc, ss));
       }
-      if (a.v_pack)
-        a.v_pack[(int64_t)r * kv_dim + idx] = f32_to_bf16_rne(x);
+      const u32x4 p1 = pack8(o1), p2 = pack8(o2);
+      if (store) {
+        uint16_t *kd = a.kc + kbase + (int64_t)g * (kBlockTokens * D);
+        *(u32x4 *)(kd + k_offset(off, 8 * j)) = p1;
+        *(u32x4 *)(kd + k_offset(off, HALF + 8 * j)) = p2;
+      }
+      if (a.k_pack) {
+        uint16_t *kp = a.k_pack + (int64_t)r * kv_dim + g * D;
+        *(u32x4 *)(kp + 8 * j) = p1;
+        *(u32x4 *)(kp + HALF + 8 * j) = p2;
+      }
     }
-    return;
+    return place;
   }
-  for (int idx = tid; idx < kv_dim; idx += nt) {
-    const int g = idx / D, d = idx % D;
-    const uint16_t v = f32_to_bf16_rne(vr[idx]);
-    if (store)
-      a.vc[vbase + (int64_t)g * (kBlockTokens * D) + v_offset(off, d)] = v;
-    if (a.v_pack)
-      a.v_pack[(int64_t)r * kv_dim + idx] = v;
+  for (int g = ((lane - 32) / 4) * n_parts + part; g < a.n_kv_heads; g += 8 * n_parts) {
+    const int q = lane % 4;
+    const f32x4 *vp = (const f32x4 *)(vr + g * D + 16 * q);
+    const f32x4 x[4] = {vp[0], vp[1], vp[2], vp[3]};
+    uint16_t h[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+      h[i] = f32_to_bf16_rne(x[i / 4][i % 4]);
+    if (a.v_pack) {
+      uint16_t *vpk = a.v_pack + (int64_t)r * kv_dim + g * D + 16 * q;
+      *(u32x4 *)vpk = pack8(h);
+      *(u32x4 *)(vpk + 8) = pack8(h + 8);
+    }
+    if (v_stage && !a.v_int8) {
+      *(u32x4 *)(v_stage + g * D + 16 * q) = pack8(h);
+      *(u32x4 *)(v_stage + g * D + 16 * q + 8) = pack8(h + 8);
+      continue;
+    }
+    if (!store)
+      continue;
+    if (a.v_int8) {
+      // The head's max |v| over its 4 lanes, then the reference's rule,
+      // getp-csrc/kernels/fast_misc.hpp:74-84.
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; i++)
+        amax = fmaxf(amax, fabsf(x[i / 4][i % 4]));
+      amax = fmaxf(amax, __shfl_xor(amax, 1));
+      amax = fmaxf(amax, __shfl_xor(amax, 2));
+      const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+      int8_t *vq = (int8_t *)a.vc + vbase + (int64_t)g * (kBlockTokens * D);
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const float c = fminf(fmaxf(rintf(x[i / 4][i % 4] * inv), -127.0f), 127.0f);
+        vq[v_int8_offset(16 * q + i, off)] = (int8_t)c;
+      }
+      if (q == 0)
+        a.vs[vbase / D + (int64_t)g * kBlockTokens + off] = amax / 127.0f;
+    } else {
+      uint16_t *vd = a.vc + vbase + (int64_t)g * (kBlockTokens * D);
+#pragma unroll
+      for (int i = 0; i < 16; i++)
+        vd[v_offset(off, 16 * q + i)] = h[i];
+    }
   }
+  return place;
 }
 
 } // namespace gkv
