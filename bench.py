@@ -300,7 +300,18 @@ def run_prefill(torch, gkv, args) -> int:
     fl = [flops(ly["window"]) for ly in layers]
     full = [i for i, ly in enumerate(layers) if not ly["window"]][0]
     dom_ms = float(np.mean([x[1] for x in kern[full]]))
-    achieved = fl[full] / (dom_ms * 1e-3) / 1e12
+    tflops = fl[full] / (dom_ms * 1e-3) / 1e12
+    # Algorithmic bytes of one prefill launch: the fp32 query of every row
+    # (the qkv rows' Q part), the packed bf16 K and V rows, the bf16 output.
+    # At ~110 FLOP per byte (full layer) this is below the MI355X ridge
+    # (2500 TFLOP/s / 8 TB/s = 312 FLOP/B): HBM is the bound of this kernel.
+    alg_bytes = float(T * Hq * D * 4 + T * Hkv * D * 2 * 2 + T * Hq * D * 2)
+    achieved = alg_bytes / (dom_ms * 1e-3) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "prefill_config4_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
     line = {
         "metric": "causal prefill attention throughput (TFLOP/s), config 4",
         "value": round(sum(fl) / (ms_per_step * 1e-3) / 1e12, 2),
@@ -320,11 +331,14 @@ def run_prefill(torch, gkv, args) -> int:
                                   for i in range(len(layers))},
             "parallelism": "1 GPU",
         },
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
-                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "prefill_kernel", "kernel_us": round(dom_ms * 1e3, 2),
-                     "algorithmic_flops": fl[full]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "kernel": "prefill_kernel",
+                     "kernel_us": round(dom_ms * 1e3, 2), "algorithmic_bytes": alg_bytes,
+                     "mfma": {"achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                              "unit": "TFLOP/s",
+                              "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                              "algorithmic_flops": fl[full]}},
         "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)

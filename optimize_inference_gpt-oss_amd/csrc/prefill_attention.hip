@@ -135,30 +135,41 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
     }
   };
 
-  // ---- query operands: column tile c holds queries q0 + 16c + n; half dh dims 32dh + 8kg + j
+  // ---- query operands: column tile c holds queries q0 + 16c + n; half dh dims 32dh + 8kg + j.
+  // The loads of both column tiles (and of their RoPE angles) and of the
+  // first K/V tile go out together: one memory round trip before compute.
   bf16x8 qhi[2][2], qlo[2][2];
   {
     const float qscale = 0.125f * kLog2e; // 1/sqrt(64); exp -> exp2
+    const bool rot = a.cos_tab != nullptr;
+    f32x4 qr[2][4], cr[2][2], sr[2][2];
 #pragma unroll
     for (int c = 0; c < 2; c++) {
       const int pos = min(q0 + 16 * c + n, L - 1);
       const float *qp = a.q + (int64_t)(row0 + pos) * a.q_stride + h * D + 8 * kg;
       // the two halves of RoPE pairs 8kg .. 8kg+7 sit in this lane
+      qr[c][0] = *(const f32x4 *)qp;
+      qr[c][1] = *(const f32x4 *)(qp + 4);
+      qr[c][2] = *(const f32x4 *)(qp + 32);
+      qr[c][3] = *(const f32x4 *)(qp + 36);
+      // without RoPE the angle loads re-read the query (any valid address)
+      const float *cp = rot ? a.cos_tab + (int64_t)pos * (D / 2) + 8 * kg : qp;
+      const float *sp = rot ? a.sin_tab + (int64_t)pos * (D / 2) + 8 * kg : qp;
+      cr[c][0] = *(const f32x4 *)cp;
+      cr[c][1] = *(const f32x4 *)(cp + 4);
+      sr[c][0] = *(const f32x4 *)sp;
+      sr[c][1] = *(const f32x4 *)(sp + 4);
+    }
+    fetch(0);
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
       float qv[2][8];
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        qv[0][j] = qp[j];
-        qv[1][j] = qp[32 + j];
-      }
-      if (a.cos_tab) {
-        const float *cp = a.cos_tab + (int64_t)pos * (D / 2) + 8 * kg;
-        const float *sp = a.sin_tab + (int64_t)pos * (D / 2) + 8 * kg;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const float x1 = qv[0][j], x2 = qv[1][j], cs = cp[j], sn = sp[j];
-          qv[0][j] = rope_first(x1, x2, cs, sn);
-          qv[1][j] = rope_second(x1, x2, cs, sn);
-        }
+        const float x1 = qr[c][j / 4][j % 4], x2 = qr[c][2 + j / 4][j % 4];
+        const float cs = cr[c][j / 4][j % 4], sn = sr[c][j / 4][j % 4];
+        qv[0][j] = rot ? rope_first(x1, x2, cs, sn) : x1;
+        qv[1][j] = rot ? rope_second(x1, x2, cs, sn) : x2;
       }
 #pragma unroll
       for (int dh = 0; dh < 2; dh++) {
@@ -181,7 +192,6 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
     for (int nn = 0; nn < 4; nn++)
       o[c][nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  fetch(0);
   stash(0);
   __syncthreads();
   for (int t = 0; t < n_tiles; t++) {
@@ -324,7 +334,8 @@ extern "C" int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_
   if (q_stride < (int64_t)n_q_heads * kHeadDim || out_stride < (int64_t)n_q_heads * kHeadDim ||
       (q_stride % 4) != 0)
     return GKV_ERR_ARG;
-  if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)q) % 16 != 0)
+  if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)q | (uintptr_t)cos_tab | (uintptr_t)sin_tab) %
+          16 != 0)
     return GKV_ERR_ARG; // 16-byte vector loads
   const int n_qblocks = (max_len + kQBlock - 1) / kQBlock;
   const int64_t grid = (int64_t)n_qblocks * B * n_kv_heads;
