@@ -26,22 +26,64 @@
 //   4kg..4kg+3 of each, which are its P^T operand slots; the V^T operand is
 //   the same 8 keys of one dim, read from V stored transposed in LDS.
 // Online softmax in the log2 domain (scale 1/8 * log2 e folded into Q), lazy
-// rescale by threshold 8, the running max seeded with the sink, and the sink
-// added in the final normalisation, as in the decode kernel.
+// rescale by threshold 8 (tested on the fp16 weights), the running max seeded
+// with the sink, and the sink added in the final normalisation, as in the
+// decode kernel. The row sums are fp32 sums of the same fp16 weights.
 //
-// LDS: K tile [64 keys][64 dims + 8 pad] bf16, V^T tile [64 dims][64 keys + 8 pad]
-// fp16, double-buffered (36 KB); tile t + 1 is fetched into registers while tile t
-// is consumed.
+// LDS (73 KB, two workgroups per CU): a pipeline of 4 K/V tile stages of 64
+// keys, fed by direct-to-LDS loads 3 tiles ahead (K and V rows as they are in
+// memory, 16-byte slots XOR-swizzled per key row); each tile's V is turned
+// into V^T [64 dims][64 keys + 8 pad] fp16 just before the tile is used.
 #include "gkv_device.hpp"
 
 namespace gkv {
 
 constexpr int kQBlock = 32;         // query positions per workgroup
 constexpr int kKTile = 64;          // keys per LDS tile
-constexpr int kKRow = kHeadDim + 8; // bf16 per K row in LDS (pad against bank conflicts)
 constexpr int kVRow = kKTile + 8;   // fp16 per V^T row in LDS
 constexpr float kVScale = 0x1p-10f; // V is staged as fp16 of v * kVScale
+constexpr int kStages = 4;          // K/V tile pipeline depth (tiles held in LDS)
+typedef __attribute__((address_space(3))) void *lds_ptr;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// s_waitcnt with vmcnt = N and the other counters left alone (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for LDS data: this wave's LDS writes complete
+// (lgkmcnt(0)), then s_barrier. Unlike __syncthreads() it does not wait for
+// the global loads in flight: a workgroup fence also waits for the tile
+// pipeline's direct-to-LDS loads, which are waited for explicitly
+// (wait_vmcnt). The empty asm statements keep the compiler from moving
+// memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); // lgkmcnt(0) only
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes land
+// at l_base + 16 l (l_base wave-uniform, held in M0). Written as asm so that
+// the compiler, which would count these loads as pending LDS stores and wait
+// for all of them before unrelated LDS reads, leaves their waits to the
+// pipeline's explicit wait_vmcnt; the compiler's own waits for its loads can
+// then only be stricter than needed, never weaker.
+__device__ __forceinline__ void dma16(const void *src, void *l_base) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr)l_base);
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\t"
+               "s_mov_b32 m0, %2\n\t"
+               "global_load_lds_dwordx4 %1, off\n\t"
+               "s_mov_b32 m0, %0" // M0 as the compiler left it
+               : "=&s"(saved)
+               : "v"(src), "s"(m)
+               : "memory");
+}
 
 struct PrefillArgs {
   const int32_t *cu;
@@ -61,9 +103,17 @@ template <int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8 ? 4 : 1))) void prefill_kernel(PrefillArgs a) {
   constexpr int D = kHeadDim;
   constexpr int NT = NW * 64;
-  constexpr int kLoads = kKTile * (D / 8) / NT; // 16-byte pieces of K (and of V) per thread per tile
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kKTile * kKRow];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][D * kVRow];
+  constexpr int kPieces = kKTile * D / 8 / NT; // V^T conversion: key pairs x 4 dims per thread
+  // The tile pipeline's stages: K and V tiles as they arrive, row-major with
+  // each 128-byte key row's 16-byte slots XOR-swizzled by key % 8 (slot s of
+  // key r holds dims 8 (s ^ (r % 8))), one array per stage so that a read of
+  // one stage waits only for that stage's loads; and V^T in fp16 for the tile
+  // being computed. 73 KB: two workgroups per CU.
+  __shared__ __attribute__((aligned(16))) uint16_t k_st0[kKTile * D], k_st1[kKTile * D],
+      k_st2[kKTile * D], k_st3[kKTile * D];
+  __shared__ __attribute__((aligned(16))) uint16_t v_st0[kKTile * D], v_st1[kKTile * D],
+      v_st2[kKTile * D], v_st3[kKTile * D];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * kVRow];
 
   int id = blockIdx.x;
   const int g = id % a.n_kv_heads;
@@ -88,48 +138,55 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   const bool active = wave < a.G;
   const int h = g * a.G + (active ? wave : 0);
 
-  // ---- K/V tile staging.
-  // K: piece i of a thread covers key (tid + i*NT) / 8, dims 8 * ((tid + i*NT) % 8).
-  // V: piece i covers keys 2pr, 2pr + 1 and dims 4pd .. 4pd+3, where virtual
-  // wave vw = (tid + i*NT) / 64 and its lane ln give pr = ln % 16 + 16 (vw % 2),
-  // pd = ln / 16 + 4 (vw / 2); the pair is stored as one dword per dim of V^T,
-  // and the 64 dwords a wave writes fall in 64 different banks.
-  u32x4 kreg[kLoads];
-  u32x2 va[kLoads], vb[kLoads];
-  auto fetch = [&](int t) {
+  // ---- K/V tile pipeline: kStages stages, tiles t+1 .. t+kStages-1 in flight while
+  // tile t is computed. Direct-to-LDS loads: lane l of a wave's load lands at
+  // byte 16 l of the wave's 1 KB chunk (8 key rows), and fetches the 16-byte
+  // slot that the swizzle puts there. Every tile slot issues its loads (rows
+  // past the prompt clamped, tiles past the last re-read), so the number of
+  // loads that follow a tile's is fixed and the wait below is exact.
+  auto k_stage = [&](int st) -> uint16_t * {
+    return st == 0 ? k_st0 : st == 1 ? k_st1 : st == 2 ? k_st2 : k_st3;
+  };
+  auto v_stage = [&](int st) -> uint16_t * {
+    return st == 0 ? v_st0 : st == 1 ? v_st1 : st == 2 ? v_st2 : v_st3;
+  };
+  auto dma = [&](int t, int st) {
     const int kt0 = k_lo + t * kKTile;
 #pragma unroll
-    for (int i = 0; i < kLoads; i++) {
-      const int idx = tid + i * NT;
-      const int key = idx >> 3, part = idx & 7;
-      const int row = row0 + min(kt0 + key, L - 1); // clamped: rows past the prompt are masked
-      kreg[i] = *(const u32x4 *)(a.k + (int64_t)row * a.kv_stride + g * D + part * 8);
-      const int vw = idx >> 6, ln = idx & 63;
-      const int pr = (ln & 15) + 16 * (vw & 1), pd = (ln >> 4) + 4 * (vw >> 1);
-      const int ra = row0 + min(kt0 + 2 * pr, L - 1), rb = row0 + min(kt0 + 2 * pr + 1, L - 1);
-      va[i] = *(const u32x2 *)(a.v + (int64_t)ra * a.kv_stride + g * D + pd * 4);
-      vb[i] = *(const u32x2 *)(a.v + (int64_t)rb * a.kv_stride + g * D + pd * 4);
+    for (int i = 0; i < 8 / NW; i++) {
+      const int chunk = wave + i * NW;
+      const int key = chunk * 8 + (lane >> 3), slot = lane & 7;
+      const int row = row0 + min(kt0 + key, L - 1);
+      const int64_t off = (int64_t)row * a.kv_stride + g * D + 8 * (slot ^ (key & 7));
+      dma16(a.k + off, k_stage(st) + chunk * 512);
+      dma16(a.v + off, v_stage(st) + chunk * 512);
     }
   };
-  // V goes to LDS as fp16 of v * 2^-10: exact for bf16 magnitudes 2^-4 .. 2^26,
-  // an absolute error of at most 2^-15 below that (fp16 subnormals), inf above
-  // (so the output shows it). P then enters the matrix core as one fp16 piece.
+  // V of a stage -> V^T as fp16 of v * 2^-10 (exact for bf16 magnitudes
+  // 2^-4 .. 2^26, an absolute error of at most 2^-15 below that, inf above,
+  // so the output shows it): P then enters the matrix core as one fp16 piece.
+  // Piece i of a thread covers keys 2pr, 2pr + 1 and dims 4pd .. 4pd+3, where
+  // virtual wave vw = (tid + i*NT) / 64 and its lane ln give
+  // pr = ln % 16 + 16 (vw % 2), pd = ln / 16 + 4 (vw / 2); the pair is one
+  // dword per dim of V^T, and the 64 dwords a wave writes fall in 64 banks.
   auto v_half = [](uint32_t bits16) -> uint32_t {
     const _Float16 h = (_Float16)(bf16_to_f32((uint16_t)bits16) * kVScale);
     return (uint32_t)__builtin_bit_cast(uint16_t, h);
   };
-  auto stash = [&](int buf) {
+  auto convert_v = [&](int st) {
+    const uint16_t *vs = v_stage(st);
 #pragma unroll
-    for (int i = 0; i < kLoads; i++) {
+    for (int i = 0; i < kPieces; i++) {
       const int idx = tid + i * NT;
-      const int key = idx >> 3, part = idx & 7;
-      *(u32x4 *)&k_lds[buf][key * kKRow + part * 8] = kreg[i];
       const int vw = idx >> 6, ln = idx & 63;
       const int pr = (ln & 15) + 16 * (vw & 1), pd = (ln >> 4) + 4 * (vw >> 1);
+      const int r0 = 2 * pr, r1 = 2 * pr + 1;
+      const u32x2 x = *(const u32x2 *)(vs + r0 * D + 8 * ((pd >> 1) ^ (r0 & 7)) + 4 * (pd & 1));
+      const u32x2 y = *(const u32x2 *)(vs + r1 * D + 8 * ((pd >> 1) ^ (r1 & 7)) + 4 * (pd & 1));
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const uint32_t wa = va[i][j >> 1] >> (16 * (j & 1)), wb = vb[i][j >> 1] >> (16 * (j & 1));
-        *(uint32_t *)&v_lds[buf][(4 * pd + j) * kVRow + 2 * pr] =
+        const uint32_t wa = x[j >> 1] >> (16 * (j & 1)), wb = y[j >> 1] >> (16 * (j & 1));
+        *(uint32_t *)&v_lds[(4 * pd + j) * kVRow + 2 * pr] =
             v_half(wa & 0xffffu) | (v_half(wb & 0xffffu) << 16);
       }
     }
@@ -160,7 +217,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
       sr[c][0] = *(const f32x4 *)sp;
       sr[c][1] = *(const f32x4 *)(sp + 4);
     }
-    fetch(0);
+#pragma unroll
+    for (int t = 0; t < kStages - 1; t++)
+      dma(t, t);
 #pragma unroll
     for (int c = 0; c < 2; c++) {
       float qv[2][8];
@@ -192,12 +251,17 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
     for (int nn = 0; nn < 4; nn++)
       o[c][nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  stash(0);
-  __syncthreads();
-  for (int t = 0; t < n_tiles; t++) {
-    const int buf = t & 1;
-    if (t + 1 < n_tiles)
-      fetch(t + 1);
+  // Tile t in stage st: wait until this wave's loads of tile t have landed
+  // (the loads of the next kStages - 2 tiles may still fly), then the barrier
+  // makes every wave's loads visible and frees the stage of tile t-1, which
+  // takes the loads of tile t + kStages - 1.
+  auto tile = [&](const int t, const int st) {
+    wait_vmcnt<(kStages - 2) * 2 * (8 / NW)>();
+    lds_barrier();
+    dma(t + kStages - 1, (st + kStages - 1) % kStages);
+    convert_v(st);
+    lds_barrier();
+    const uint16_t *ks = k_stage(st);
     const int kt0 = k_lo + t * kKTile;
 #pragma unroll
     for (int s = 0; s < kKTile / 32; s++) {
@@ -213,8 +277,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
         acc[kt][0] = acc[kt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int dh = 0; dh < 2; dh++) {
-          const bf16x8 kop =
-              *(const bf16x8 *)&k_lds[buf][(32 * s + 16 * kt + n) * kKRow + 32 * dh + 8 * kg];
+          const int kr = 32 * s + 16 * kt + n; // key row; its dims 32dh + 8kg .. +7
+          const bf16x8 kop = *(const bf16x8 *)&ks[kr * D + 8 * ((4 * dh + kg) ^ (kr & 7))];
 #pragma unroll
           for (int c = 0; c < 2; c++) {
             acc[kt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[c][dh], acc[kt][c], 0, 0, 0);
@@ -232,24 +296,34 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
           for (int r = 0; r < 4; r++)
             sc[4 * kt + r] = acc[kt][c][r];
         if (need_mask) {
-          const int qa = q0 + 16 * c + n;
+          // key ka is kept iff 0 <= qa - ka < W (no window: below 2^31), one
+          // unsigned compare per score
+          const uint32_t wlim = W > 0 ? (uint32_t)W : 0x80000000u;
+          const int back0 = (q0 + 16 * c + n) - (kb + 4 * kg); // qa - ka of slot 0
 #pragma unroll
           for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-              const int ka = kb + 16 * kt + 4 * kg + r;
-              if (ka > qa || (W > 0 && ka <= qa - W))
+            for (int r = 0; r < 4; r++)
+              if ((uint32_t)(back0 - 16 * kt - r) >= wlim)
                 sc[4 * kt + r] = -INFINITY;
-            }
         }
-        float mx = sc[0];
 #pragma unroll
-        for (int i = 1; i < 8; i++)
-          mx = fmaxf(mx, sc[i]);
-        // lazy rescale: the reference max moves only when exceeded by more than 8;
-        // the test needs no cross-lane max (m_run is the same in the 4 lanes of
-        // a column), only the rescale does
-        if (__any(mx > m_run[c] + 8.0f)) {
+        for (int i = 0; i < 8; i++)
+          ph[c][i] = (_Float16)__builtin_amdgcn_exp2f(sc[i] - m_run[c]);
+        // Lazy rescale: the reference max moves only when a weight exceeds 2^8
+        // (a score more than 8 above it; an fp16 weight of inf included). The
+        // test runs on the fp16 weights with packed max; it needs no cross-lane
+        // max (m_run is the same in the 4 lanes of a column), only the rescale,
+        // which then recomputes the weights.
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        f16x2 w2 = __builtin_elementwise_max(
+            __builtin_elementwise_max(f16x2{ph[c][0], ph[c][1]}, f16x2{ph[c][2], ph[c][3]}),
+            __builtin_elementwise_max(f16x2{ph[c][4], ph[c][5]}, f16x2{ph[c][6], ph[c][7]}));
+        if (__any(__builtin_elementwise_max(w2[0], w2[1]) > (_Float16)256.0f)) {
+          float mx = sc[0];
+#pragma unroll
+          for (int i = 1; i < 8; i++)
+            mx = fmaxf(mx, sc[i]);
           mx = fmaxf(mx, __shfl_xor(mx, 16));
           mx = fmaxf(mx, __shfl_xor(mx, 32));
           const float m_new = fmaxf(m_run[c], mx);
@@ -259,17 +333,19 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
 #pragma unroll
           for (int nn = 0; nn < 4; nn++)
             o[c][nn] *= alpha;
-        }
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const float p = __builtin_amdgcn_exp2f(sc[i] - m_run[c]);
-          lsum[c] += p;
-          ph[c][i] = (_Float16)p;
+          for (int i = 0; i < 8; i++)
+            ph[c][i] = (_Float16)__builtin_amdgcn_exp2f(sc[i] - m_run[c]);
         }
+        // the row sum of the same fp16 weights the output uses (fp32 sums)
+#pragma unroll
+        for (int i = 0; i < 8; i += 2)
+          lsum[c] = __builtin_amdgcn_fdot2(f16x2{ph[c][i], ph[c][i + 1]},
+                                           f16x2{(_Float16)1.0f, (_Float16)1.0f}, lsum[c], false);
       }
 #pragma unroll
       for (int nn = 0; nn < 4; nn++) {
-        const uint16_t *vrow = &v_lds[buf][(16 * nn + n) * kVRow + 32 * s + 4 * kg];
+        const uint16_t *vrow = &v_lds[(16 * nn + n) * kVRow + 32 * s + 4 * kg];
         const u32x2 x = *(const u32x2 *)vrow;
         const u32x2 y = *(const u32x2 *)(vrow + 16);
         const f16x8 vop = __builtin_bit_cast(f16x8, u32x4{x[0], x[1], y[0], y[1]});
@@ -278,10 +354,15 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
           o[c][nn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, ph[c], o[c][nn], 0, 0, 0);
       }
     }
-    if (t + 1 < n_tiles)
-      stash(buf ^ 1);
-    __syncthreads();
+  };
+  for (int t = 0; t < n_tiles; t += kStages) {
+    tile(t, 0);
+#pragma unroll
+    for (int st = 1; st < kStages; st++)
+      if (t + st < n_tiles)
+        tile(t + st, st);
   }
+  wait_vmcnt<0>(); // no load may still write into LDS when the workgroup ends
   if (!active)
     return;
 
