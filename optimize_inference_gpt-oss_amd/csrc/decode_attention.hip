@@ -77,6 +77,8 @@ constexpr int kPlanHeader = 4;         // ints: T, S, workgroups used, unused
 constexpr int kIdRegs = 4;             // block-id registers per wave: ranges of <= 4096 tokens
 constexpr int kMaxRange = kIdRegs * 64 * kBlockTokens;
 constexpr int kInfoRegs = kMaxRange / kStep / 64; // step-record registers
+constexpr int kIdSlab = kIdRegs * 64;     // block ids per range (its slab in the workspace)
+constexpr int kInfoSlab = kInfoRegs * 64; // step records per range
 constexpr int kSplitWaves = 4;         // split kernel: one wave per SIMD
 constexpr int kSplitThreads = 64 * kSplitWaves;
 constexpr int kPrepThreads = 1024;
@@ -106,8 +108,9 @@ struct DecodeArgs {
   int n_wg;           // split workgroups launched
   int fixed_S;        // 0: S = T / n_wg (balanced); > 0: this S
   int32_t *plan;      // [kPlanHeader][cu: B + 1]
-  int32_t *flat;      // block id of every 16-token block of the stream
-  int32_t *steps;     // step record of every 32-token step of the stream
+  int32_t *flat;      // block id of every 16-token block of the stream, per range:
+                      // [range][kIdSlab], block k of range w at w * kIdSlab + k
+  int32_t *steps;     // step record of every 32-token step: [range][kInfoSlab]
   u32x4 *qops;        // [B][Hkv][64 lanes][2]: query operands
   float *ws_o;        // [B + kMaxWorkgroups][Hkv][8][64]
   float *ws_ml;       // [B + kMaxWorkgroups][Hkv][8][2]
@@ -294,10 +297,11 @@ __device__ __forceinline__ void prep_blocks(const DecodeArgs &a, int wg, int n_w
         any_bad = true;
       }
     }
-    a.flat[e] = id;
+    const int w = tok / S; // the range, and the block's place in its slab
+    a.flat[w * kIdSlab + (tok - w * S) / kBlockTokens] = id;
     if ((e & 1) == 0)
-      a.steps[e >> 1] = step_record(b, off == 0, tok + kStep == s_cu[b + 1],
-                                    min(max(n - off, 0), kStep));
+      a.steps[w * kInfoSlab + (tok - w * S) / kStep] =
+          step_record(b, off == 0, tok + kStep == s_cu[b + 1], min(max(n - off, 0), kStep));
   }
   if (any_bad && a.dev_err)
     atomicOr(a.dev_err, GKV_DEVERR_BLOCK_ID);
@@ -348,6 +352,17 @@ __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(1
 void decode_split_kernel(DecodeArgs a) {
   constexpr int D = kHeadDim;
   const int w_id = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  // Block ids and step records of the range, one per lane per register. The
+  // range's slab needs no plan to be found, so these loads go out with the
+  // plan's; entries past the range's steps are never read.
+  int tv[kIdRegs], ti[kInfoRegs];
+#pragma unroll
+  for (int i = 0; i < kIdRegs; i++)
+    tv[i] = a.flat[w_id * kIdSlab + 64 * i + lane];
+#pragma unroll
+  for (int i = 0; i < kInfoRegs; i++)
+    ti[i] = a.steps[w_id * kInfoSlab + 64 * i + lane];
   const int T = a.plan[0], S = a.plan[1];
   const int rs = w_id * S;
   if (rs >= T)
@@ -355,7 +370,6 @@ void decode_split_kernel(DecodeArgs a) {
   const int re = min(rs + S, T);
   const int n_steps = (re - rs) / kStep; // every sequence is padded to whole steps
 
-  const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // wave-uniform
   const int n_waves = blockDim.x >> 6;
   const int col = lane & 15, kg = lane >> 4;
@@ -370,15 +384,6 @@ void decode_split_kernel(DecodeArgs a) {
   const size_t head_bytes = (size_t)kBlockTokens * D * 2;               // 2 KB
   const uint32_t vq_off = (uint32_t)(col * 4 + kg) * 16;                 // int8 V piece
 
-  // Block ids and step records of the range, one per lane per register.
-  const int e0 = rs / kBlockTokens, s0 = rs / kStep;
-  int tv[kIdRegs], ti[kInfoRegs];
-#pragma unroll
-  for (int i = 0; i < kIdRegs; i++)
-    tv[i] = a.flat[e0 + min(64 * i + lane, 2 * n_steps - 1)];
-#pragma unroll
-  for (int i = 0; i < kInfoRegs; i++)
-    ti[i] = a.steps[s0 + min(64 * i + lane, n_steps - 1)];
 
   auto pick = [&](const int *regs, int nregs, int j) -> int {
     const int w = j >> 6, l = j & 63;
@@ -771,8 +776,8 @@ static WorkspaceLayout layout_of(int B, int n_kv_heads, int64_t t_max) {
   WorkspaceLayout L;
   L.plan = 0;
   L.flat = align256((size_t)(kPlanHeader + B + 1) * 4);
-  L.steps = L.flat + align256((size_t)(t_max / kBlockTokens + 1) * 4);
-  L.qops = L.steps + align256((size_t)(t_max / kStep + 1) * 4);
+  L.steps = L.flat + align256((size_t)kMaxWorkgroups * kIdSlab * 4);
+  L.qops = L.steps + align256((size_t)kMaxWorkgroups * kInfoSlab * 4);
   L.ws_o = L.qops + align256((size_t)B * n_kv_heads * 64 * 32);
   const size_t parts = (size_t)(B + kMaxWorkgroups) * n_kv_heads;
   L.ws_ml = L.ws_o + parts * kPartFloats * sizeof(float);
