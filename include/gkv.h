@@ -219,7 +219,11 @@ int gkv_decode_layer_prepare(void *stream, int32_t B, int32_t n_q_heads, const f
  *   cos_tab/sin_tab  NULL (both), or device copies of gkv_rope_table rows
  *   k, v     bf16 [rows][Hkv][64] (gkv_kv_append's k_pack, v_pack)
  *   cu_seqlens device int32 [B+1]; max_len = host bound of the prompt lengths
- *   out      [rows][out_stride] of out_dtype */
+ *   out      [rows][out_stride] of out_dtype
+ * q, k, v and the tables are 16-byte aligned, q_stride a multiple of 4
+ * (GKV_ERR_ARG otherwise). V enters an fp16 matrix core as v * 2^-10: exact
+ * for bf16 magnitudes 2^-4 .. 2^26, an absolute error of at most 2^-15 below,
+ * inf above (which the output shows). */
 int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_seqlens, int32_t max_len,
                           int32_t n_q_heads, int32_t n_kv_heads, const float *q,
                           int64_t q_stride, const float *cos_tab, const float *sin_tab,

@@ -165,6 +165,16 @@ def test_group_sizes(oracle, gkv, cuda, Hq, Hkv):
     check(case, run_gpu(case, gkv, torch, cuda))
 
 
+@pytest.mark.parametrize("window", [0, 128])
+def test_long_prompts(oracle, gkv, cuda, window):
+    """Prompts of 1,000-2,000 rows: 16-32 key tiles per query block, so the
+    4-stage K/V tile pipeline wraps many times (and its past-the-end loads
+    re-read the last rows)."""
+    import torch
+    case = PrefillCase(oracle, 60 + window, [2000, 1031, 64], 64, 8, window=window)
+    check(case, run_gpu(case, gkv, torch, cuda))
+
+
 def test_large_scores_bf16_out(oracle, gkv, cuda):
     """Scores spread over tens of units (peaked softmax, rescales), bf16 output."""
     import torch
