@@ -220,43 +220,58 @@ __device__ __forceinline__ void prep_query_items(const DecodeArgs &a, int wg, in
 // stream blocks; workgroup 0 also publishes the plan. wg / n_wgs: this
 // workgroup's index among the block workgroups and their count.
 __device__ __forceinline__ void prep_blocks(const DecodeArgs &a, int wg, int n_wgs) {
+  constexpr int kWaves = kPrepThreads / 64;
+  constexpr int kPer = (kMaxBatch + kPrepThreads - 1) / kPrepThreads;
   __shared__ int s_cu[kMaxBatch + 1];
-  __shared__ int s_scan[2][kPrepThreads];
-  const int t = threadIdx.x, B = a.B;
+  __shared__ int s_wave[kWaves];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, B = a.B;
   const int per = (B + kPrepThreads - 1) / kPrepThreads;
   const int b0 = t * per;
+  // padded lengths of this thread's sequences, kept in registers for the
+  // second pass (a reload after the barriers would be one more round trip)
+  int len[kPer];
   int local = 0;
   bool any_over = false;
-  for (int i = 0; i < per; i++) {
-    const int b = b0 + i;
-    if (b < B) {
+#pragma unroll
+  for (int i = 0; i < kPer; i++) {
+    len[i] = 0;
+    if (i < per && b0 + i < B) {
       bool over;
-      local += pad_step(seq_tokens(a, b, &over));
+      len[i] = pad_step(seq_tokens(a, b0 + i, &over));
       any_over |= over;
     }
+    local += len[i];
   }
   if (any_over && wg == 0 && a.dev_err)
     atomicOr(a.dev_err, GKV_DEVERR_LENGTH);
-  // inclusive scan of the per-thread sums (Hillis-Steele, double buffered)
-  int buf = 0;
-  s_scan[0][t] = local;
-  __syncthreads();
-  for (int off = 1; off < kPrepThreads; off <<= 1) {
-    const int v = s_scan[buf][t] + (t >= off ? s_scan[buf][t - off] : 0);
-    s_scan[buf ^ 1][t] = v;
-    buf ^= 1;
-    __syncthreads();
+  // inclusive scan: within each wave by shuffles, then over the wave totals
+  int incl = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int v = __shfl_up(incl, off, 64);
+    if (lane >= off)
+      incl += v;
   }
-  int run = s_scan[buf][t] - local;
-  for (int i = 0; i < per; i++) {
-    const int b = b0 + i;
-    if (b < B) {
-      s_cu[b] = run;
-      run += pad_step(seq_tokens(a, b));
+  if (lane == 63)
+    s_wave[wave] = incl;
+  __syncthreads();
+  int before = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; w++) {
+    const int v = s_wave[w];
+    before += w < wave ? v : 0;
+    total += v;
+  }
+  int run = before + incl - local;
+#pragma unroll
+  for (int i = 0; i < kPer; i++) {
+    if (i < per && b0 + i < B) {
+      s_cu[b0 + i] = run;
+      run += len[i];
     }
   }
-  if (t == kPrepThreads - 1)
-    s_cu[B] = s_scan[buf][t];
+  if (t == 0)
+    s_cu[B] = total;
   __syncthreads();
   const int T = s_cu[B];
   int S = a.fixed_S;
@@ -330,7 +345,9 @@ __global__ __launch_bounds__(kPrepThreads) void decode_layer_prep_kernel(DecodeA
                                                                          int n_rows,
                                                                          int n_app,
                                                                          int n_qwg) {
-  const int wg = blockIdx.x;
+  // block workgroups first: theirs is the longest chain of dependent loads
+  const int n_bwg = gridDim.x - n_app - n_qwg;
+  const int wg = ((int)blockIdx.x + n_app + n_qwg) % gridDim.x;
   if (wg < n_app) {
     const int wave = threadIdx.x >> 6;
     const int r = wg * kAppendRowsPerWg + wave / kAppendWavesPerRow;
@@ -339,7 +356,7 @@ __global__ __launch_bounds__(kPrepThreads) void decode_layer_prep_kernel(DecodeA
   } else if (wg < n_app + n_qwg) {
     prep_query_items(a, wg - n_app, n_qwg);
   } else {
-    prep_blocks(a, wg - n_app - n_qwg, gridDim.x - n_app - n_qwg);
+    prep_blocks(a, wg - n_app - n_qwg, n_bwg);
   }
 }
 
