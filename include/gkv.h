@@ -12,6 +12,9 @@
  *                            (run.cpp:422-504)
  *   gkv_kv_append         <- rope_kv_bf16, getp-csrc/kernels/fast_misc.hpp:112-127
  *                            (and rope_exact + kv_write_kernel, kernels/misc.hpp:55-85)
+ *   gkv_qkv_append        <- the pair gemm_bf16 (getp-csrc/kernels/fast_gemm.hpp:888-899)
+ *                            + rope_kv_bf16 in layer_attention, gpu_engine.hpp:493-496
+ *                            (one launch: the append in the projection's epilogue)
  *   gkv_decode_attention  <- attention_q8v_chunk64 / attention_bf16_chunk64 / attention_bf16,
  *                            getp-csrc/kernels/fast_attention.hpp:604-622, 566-580, 525-547
  *   gkv_decode_layer      <- the pair rope_kv_bf16 + attention_q8v_chunk64 in layer_attention,
@@ -131,6 +134,25 @@ int gkv_kv_append(void *stream, int32_t n_rows, const float *qkv, int64_t row_st
                   const int32_t *row_pos, const int32_t *row_seq, const int32_t *seq_lens,
                   gkv_cache_view cache, float *q_out, int64_t q_out_stride, void *k_pack,
                   void *v_pack, uint32_t *dev_err);
+
+/* QKV projection with the append in its epilogue: for each row r,
+ *   qkv[r][i] = sum_j x[r][j] * w_qkv[i][j] + b_qkv[i]
+ * (fp32 accumulation of bf16 products, the bias added to the finished sum, as
+ * gemm_bf16 computes it; i < (Hq + 2 Hkv) * 64), written to qkv_out (fp32
+ * [rows][out_stride], NULL: not written), and the row's K part rotated and its
+ * K and V parts stored into the paged cache exactly as gkv_kv_append stores
+ * the same qkv row (cache.k == cache.v == NULL: no append). Row placement
+ * (row_pos, row_seq, seq_lens, the ring rule, dev_err) is gkv_kv_append's;
+ * with row_pos NULL, row r sits at position seq_lens[seq]-1 (a decode step).
+ *   x      bf16 [rows][x_stride], x_stride a multiple of 8, 16-byte aligned
+ *   w_qkv  bf16 [(Hq + 2 Hkv) * 64][hidden] row-major, 16-byte aligned
+ *   b_qkv  fp32 [(Hq + 2 Hkv) * 64] or NULL
+ * hidden is a multiple of 64 (GKV_ERR_UNSUPPORTED otherwise). */
+int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64_t x_stride,
+                   int32_t hidden, const void *w_qkv, const float *b_qkv, int32_t n_q_heads,
+                   const float *cos_tab, const float *sin_tab, const int32_t *row_pos,
+                   const int32_t *row_seq, const int32_t *seq_lens, gkv_cache_view cache,
+                   float *qkv_out, int64_t out_stride, uint32_t *dev_err);
 
 /* ---- Decode attention ---------------------------------------------------- */
 

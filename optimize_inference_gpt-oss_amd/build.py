@@ -25,6 +25,7 @@ SOURCES = [
     "kv_append.hip",
     "decode_attention.hip",
     "prefill_attention.hip",
+    "qkv_append.hip",
     "rope_table.cpp",
     "kv_pool.cpp",
     "capi.cpp",

@@ -35,6 +35,7 @@
 // memory, 16-byte slots XOR-swizzled per key row); each tile's V is turned
 // into V^T [64 dims][64 keys + 8 pad] fp16 just before the tile is used.
 #include "gkv_device.hpp"
+#include "lds_dma.hpp"
 
 namespace gkv {
 
@@ -43,47 +44,7 @@ constexpr int kKTile = 64;          // keys per LDS tile
 constexpr int kVRow = kKTile + 8;   // fp16 per V^T row in LDS
 constexpr float kVScale = 0x1p-10f; // V is staged as fp16 of v * kVScale
 constexpr int kStages = 4;          // K/V tile pipeline depth (tiles held in LDS)
-typedef __attribute__((address_space(3))) void *lds_ptr;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-
-// s_waitcnt with vmcnt = N and the other counters left alone (gfx9 encoding:
-// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// Workgroup barrier for LDS data: this wave's LDS writes complete
-// (lgkmcnt(0)), then s_barrier. Unlike __syncthreads() it does not wait for
-// the global loads in flight: a workgroup fence also waits for the tile
-// pipeline's direct-to-LDS loads, which are waited for explicitly
-// (wait_vmcnt). The empty asm statements keep the compiler from moving
-// memory accesses across the barrier.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); // lgkmcnt(0) only
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// 16 bytes per lane from global memory straight into LDS: lane l's bytes land
-// at l_base + 16 l (l_base wave-uniform, held in M0). Written as asm so that
-// the compiler, which would count these loads as pending LDS stores and wait
-// for all of them before unrelated LDS reads, leaves their waits to the
-// pipeline's explicit wait_vmcnt; the compiler's own waits for its loads can
-// then only be stricter than needed, never weaker.
-__device__ __forceinline__ void dma16(const void *src, void *l_base) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr)l_base);
-  uint32_t saved;
-  asm volatile("s_mov_b32 %0, m0\n\t"
-               "s_mov_b32 m0, %2\n\t"
-               "global_load_lds_dwordx4 %1, off\n\t"
-               "s_mov_b32 m0, %0" // M0 as the compiler left it
-               : "=&s"(saved)
-               : "v"(src), "s"(m)
-               : "memory");
-}
 
 struct PrefillArgs {
   const int32_t *cu;

@@ -82,6 +82,8 @@ SIGNATURES = {
     "gkv_rope_table": (ctypes.c_int, [ctypes.POINTER(RopeConfig), _i32, _vp, _vp]),
     "gkv_kv_append": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp,
                                      CacheView, _vp, _i64, _vp, _vp, _vp]),
+    "gkv_qkv_append": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp,
+                                      _vp, _vp, _vp, CacheView, _vp, _i64, _vp]),
     "gkv_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
     "gkv_decode_attention": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
                                             CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64,
@@ -222,6 +224,22 @@ def kv_append(qkv, n_q_heads, cos_tab, sin_tab, row_pos, view: CacheView, row_se
                              ptr(seq_lens), view, ptr(q_out), q_stride, ptr(k_pack), ptr(v_pack),
                              ptr(dev_err))
     check("gkv_kv_append", st)
+
+
+def qkv_append(x, w_qkv, b_qkv, n_q_heads, cos_tab, sin_tab, view: CacheView | None,
+               row_pos=None, row_seq=None, seq_lens=None, qkv_out=None, dev_err=None,
+               stream=None, n_kv_heads=None):
+    """gkv_qkv_append: qkv = x . w_qkv^T + b_qkv (x bf16 [rows, hidden], w_qkv bf16
+    [(Hq + 2 Hkv) 64, hidden]) into qkv_out (fp32, optional), and the rotated K
+    and the V of each row into the paged cache of `view` (optional)."""
+    if view is None:  # projection only
+        view = CacheView(n_kv_heads=n_kv_heads)
+    out_stride = qkv_out.stride(0) if qkv_out is not None else 0
+    st = lib().gkv_qkv_append(stream_handle(stream), x.shape[0], ptr(x), x.stride(0), x.shape[1],
+                              ptr(w_qkv), ptr(b_qkv), n_q_heads, ptr(cos_tab), ptr(sin_tab),
+                              ptr(row_pos), ptr(row_seq), ptr(seq_lens), view, ptr(qkv_out),
+                              out_stride, ptr(dev_err))
+    check("gkv_qkv_append", st)
 
 
 def workspace_bytes(B, n_kv_heads, max_seq_len, window=0, split_tokens=0) -> int:

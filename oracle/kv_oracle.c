@@ -23,6 +23,10 @@
  *       position (it is defined as that); brute force fp64 on tiny prompts.
  *   orc_kv_append  bit-exact vs run.cpp (_ref: the key written into the
  *       cache by forward()) and the bf16 rule above.
+ *   orc_linear     bit-exact vs run.cpp matmul + bias add (_ref); closed forms:
+ *       a one-hot input row gives W's column plus the bias exactly; products
+ *       of bf16 values are exact, so it equals an fp64 sum rounded once to
+ *       fp32 (numpy) before the bias.
  *   orc_quantize_v  bit-exact vs the reference's own quantize_v
  *       (getp-csrc/tests/attn_test.cpp, built into oracle/_ref/libref_q8.so)
  *       on random heads; closed forms: exact multiples of the step, the amax
@@ -292,5 +296,28 @@ void orc_quantize_v(const float *v, int n_heads, int head_dim, int8_t *codes, fl
       codes[(long)h * head_dim + i] = (int8_t)c;
     }
     scales[h] = amax / 127.0f;
+  }
+}
+
+/* qkv rows of the QKV projection: out[r][i] = fp32(sum_j fp32(w[i][j] x[r][j]))
+ * in a double accumulator, then + bias[i] in fp32 (run.cpp:355-367 matmul,
+ * run.cpp:565-570 bias add), for n_rows input rows. */
+void orc_linear(int n_rows, const float *x, long x_stride, const float *w, const float *bias,
+                int n_in, int n_out, float *out, long out_stride) {
+  long idx;
+#pragma omp parallel for private(idx)
+  for (idx = 0; idx < (long)n_rows * n_out; idx++) {
+    const long r = idx / n_out, i = idx % n_out;
+    const float *xr = x + r * x_stride;
+    const float *wi = w + i * (long)n_in;
+    double val = 0.0;
+    for (int j = 0; j < n_in; j++) {
+      const float prod = wi[j] * xr[j];
+      val += prod;
+    }
+    float o = (float)val;
+    if (bias)
+      o += bias[i];
+    out[r * out_stride + i] = o;
   }
 }

@@ -89,6 +89,8 @@ int orc_prefill_attention(int B, int n_q_heads, int n_kv_heads, int head_dim,
  * Outputs per sequence (kv_dim = Hkv*d): k_rot (fp32 rotated K, may be NULL),
  * k_bf16 and v_bf16 ([b*kv_dim + g*d + i]); q_rot (fp32 rotated Q, may be
  * NULL, [b*Hq*d + h*d + i]). */
+void orc_linear(int n_rows, const float *x, long x_stride, const float *w, const float *bias,
+                int n_in, int n_out, float *out, long out_stride);
 void orc_kv_append(int B, int n_q_heads, int n_kv_heads, int head_dim, const float *qkv,
                    long row_stride, const float *cos_tab, const float *sin_tab, const int *pos,
                    float *q_rot, float *k_rot, uint16_t *k_bf16, uint16_t *v_bf16);

@@ -61,6 +61,7 @@ def lib():
                                             _vp, _l, _i]
         L.orc_prefill_attention.restype = _i
         L.orc_quantize_v.argtypes = [_vp, _i, _i, _vp, _vp]
+        L.orc_linear.argtypes = [_i, _vp, _l, _vp, _vp, _i, _i, _vp, _l]
         L.orc_kv_append.argtypes = [_i, _i, _i, _i, _vp, _l, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
         _lib = L
     return _lib
@@ -79,6 +80,7 @@ def ref():
         R.ref_yarn.argtypes = [_f, _i, _f, _f, _f, _f, _vp, _vp]
         R.ref_rotate.argtypes = [_vp, _vp, _vp, _i, _i]
         R.ref_softmax.argtypes = [_vp, _i]
+        R.ref_matmul_bias.argtypes = [_vp, _vp, _vp, _vp, _i, _i]
         R.ref_decode_one.argtypes = [_i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp]
         R.ref_decode_one.restype = _i
         _ref = R
@@ -196,6 +198,21 @@ def prefill_attention(cu_seqlens, q, k, v, sinks, window=0, n_threads=0):
     return out
 
 
+def linear(x, w, bias=None):
+    """x [rows, n_in], w [n_out, n_in] fp32 (bf16 values for the QKV
+    projection), bias [n_out] or None -> [rows, n_out] fp32 (run.cpp matmul +
+    bias add)."""
+    x, w = _f32(x), _f32(w)
+    rows, n_in = x.shape
+    n_out = w.shape[0]
+    assert w.shape[1] == n_in
+    out = np.zeros((rows, n_out), np.float32)
+    b = None if bias is None else _f32(bias)
+    lib().orc_linear(rows, _p(x), n_in, _p(w), None if b is None else _p(b), n_in, n_out,
+                     _p(out), n_out)
+    return out
+
+
 def kv_append(qkv, n_q_heads, n_kv_heads, cos_tab, sin_tab, pos, head_dim=64):
     """qkv [B, (Hq + 2 Hkv) d] fp32. Returns q_rot, k_rot, k_bf16, v_bf16."""
     qkv = _f32(qkv)
@@ -252,6 +269,17 @@ def ref_softmax(x):
     y = _f32(x).copy()
     ref().ref_softmax(_p(y), y.size)
     return y
+
+
+def ref_matmul_bias(x_row, w, bias=None):
+    """run.cpp matmul of one input row plus the bias add (the reference's own code)."""
+    x = _f32(x_row).copy()
+    w = _f32(w).copy()
+    n_out, n_in = w.shape
+    out = np.zeros(n_out, np.float32)
+    b = None if bias is None else _f32(bias).copy()
+    ref().ref_matmul_bias(_p(out), _p(x), _p(w), None if b is None else _p(b), n_in, n_out)
+    return out
 
 
 def ref_decode_one(qkv_row, k_hist, v_hist, sinks, pos, n_q_heads, n_kv_heads, window=128,

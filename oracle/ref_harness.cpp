@@ -32,6 +32,15 @@ void ref_rotate(float *x, float *cosv, float *sinv, int n_heads, int head_dim) {
 
 void ref_softmax(float *x, int size) { softmax(x, size); }
 
+// run.cpp's QKV projection of one row: matmul (run.cpp:355-367), then the
+// bias add of forward() (run.cpp:565-570).
+void ref_matmul_bias(float *out, float *x, float *w, const float *bias, int n_in, int n_out) {
+  matmul(out, x, w, n_in, n_out);
+  if (bias)
+    for (int i = 0; i < n_out; ++i)
+      out[i] += bias[i];
+}
+
 // One decode step of one sequence through run.cpp forward().
 //   window_layer: 1 -> the attention runs on layer 0 (a sliding-window layer
 //   when window > 0), 0 -> on layer 1 (full attention).

@@ -302,3 +302,45 @@ def test_quantize_v_matches_reference_build():
         codes, scales = O.quantize_v(v.reshape(1, 64))
         rc, rs = O.ref_quantize_v(v)
         assert np.array_equal(codes[0], rc) and np.float32(scales[0]) == np.float32(rs)
+
+
+# ---- orc_linear (QKV projection: run.cpp matmul + bias add) ----------------
+
+def _bf16_values(a):
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    return u.view(np.float32)
+
+
+def test_linear_matches_reference_matmul(oracle):
+    """Bit-exact against run.cpp's own matmul + bias add (oracle/_ref)."""
+    if not oracle.ref_available():
+        pytest.skip("oracle/_ref not built (no reference sources)")
+    rng = np.random.default_rng(21)
+    x = _bf16_values(rng.standard_normal((4, 576)))
+    w = _bf16_values(rng.standard_normal((320, 576)) * 0.05)
+    b = (rng.standard_normal(320) * 0.1).astype(np.float32)
+    got = oracle.linear(x, w, b)
+    for r in range(4):
+        ref = oracle.ref_matmul_bias(x[r], w, b)
+        assert np.array_equal(got[r].view(np.uint32), ref.view(np.uint32))
+
+
+def test_linear_closed_forms(oracle):
+    """A one-hot row picks W's column exactly (plus the bias in fp32); with bf16
+    inputs every product is exact, so the result is the fp64 sum rounded once
+    to fp32, then the bias added in fp32."""
+    rng = np.random.default_rng(22)
+    n_in, n_out = 192, 128
+    w = _bf16_values(rng.standard_normal((n_out, n_in)))
+    b = rng.standard_normal(n_out).astype(np.float32)
+    x = np.zeros((3, n_in), np.float32)
+    x[0, 5] = 1.0
+    x[1, 191] = -2.0
+    x[2] = _bf16_values(rng.standard_normal(n_in))
+    got = oracle.linear(x, w, b)
+    assert np.array_equal(got[0], (w[:, 5] + b).astype(np.float32))
+    assert np.array_equal(got[1], (np.float32(-2.0) * w[:, 191] + b).astype(np.float32))
+    exact = (x[2].astype(np.float64) @ w.astype(np.float64).T).astype(np.float32) + b
+    assert np.array_equal(got[2].view(np.uint32), exact.view(np.uint32))
+    assert np.array_equal(oracle.linear(x, w, None)[0], w[:, 5])
