@@ -346,6 +346,93 @@ def run_prefill(torch, gkv, args) -> int:
     return 0
 
 
+def run_qkv(torch, gkv, args) -> int:
+    """The QKV projection of a config-2 decode step with the append in its
+    epilogue (gkv_qkv_append): 512 rows of x (bf16, hidden 2880, gpt-oss-20b)
+    times W_qkv (bf16 [5120, 2880]) plus bias into fp32 qkv rows, and each row's
+    rotated K and its V into the paged cache at position seq_lens[b]-1. Beside it:
+    the unfused pair as a caller would run it without this entry point, a
+    library GEMM (torch.mm, bf16) and gkv_kv_append."""
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[2]
+    B, Hq, Hkv, hidden = cfg["B"], cfg["Hq"], cfg["Hkv"], 2880
+    N = (Hq + 2 * Hkv) * D
+    rng = np.random.default_rng(args.seed)
+    L = rng.integers(cfg["lo"], cfg["hi"] + 1, size=B).astype(np.int32)
+    seq_lens = L + 1
+    max_len = int(seq_lens.max())
+    pool = gkv.Pool(n_layers=1, n_kv_heads=Hkv, max_seqs=B, max_seq_len=max_len, window=0,
+                    num_blocks=int(((seq_lens + 15) // 16).sum()) + 64,
+                    shuffle_seed=args.seed)
+    for b in range(B):
+        assert pool.seq_alloc() == b
+        if pool.reserve(b, int(seq_lens[b])) != 0:
+            raise RuntimeError("pool reserve failed")
+    pool.sync()
+    view = pool.view(0)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+    cos, sin = gkv.rope_table(max_len)
+    cos_d, sin_d, lens_d = t(cos), t(sin), t(seq_lens)
+    pos_d = t(seq_lens - 1)
+    g = torch.Generator(device=dev)
+    g.manual_seed(args.seed)
+    x = torch.randn(B, hidden, generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn(N, hidden, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g, device=dev) * 0.1
+    qkv = torch.empty(B, N, dtype=torch.float32, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def fused():
+        gkv.qkv_append(x, w, bias, Hq, cos_d, sin_d, view, seq_lens=lens_d, qkv_out=qkv,
+                       dev_err=err)
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    ms = timed(fused)
+    if int(err.item()) != 0:
+        raise RuntimeError(f"device error word {int(err.item())}")
+    lib_ms = timed(lambda: torch.mm(x, w.t()))
+    app_ms = timed(lambda: gkv.kv_append(qkv, Hq, cos_d, sin_d, pos_d, view, seq_lens=lens_d))
+    flops = 2.0 * B * N * hidden
+    tflops = flops / (ms * 1e-3) / 1e12
+    alg_bytes = float(B * hidden * 2 + N * hidden * 2 + N * 4 + B * N * 4 + B * Hkv * D * 2 * 2)
+    line = {
+        "metric": "QKV projection + KV append throughput (TFLOP/s), config-2 decode rows",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) x, N(0,1)*0.02 W, N(0,1)*0.1 bias, permuted blocks)",
+        "config": {"workload": "gkv_qkv_append on config 2's decode rows (gpt-oss-20b "
+                               "hidden 2880)", "rows": B, "hidden": hidden, "N": N,
+                   "unfused_ms": {"torch.mm bf16 (library GEMM, bf16 out)": round(lib_ms, 4),
+                                  "gkv_kv_append": round(app_ms, 4)},
+                   "parallelism": "1 GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "qkv_append_kernel", "kernel_us": round(ms * 1e3, 2),
+                     "algorithmic_flops": flops,
+                     "hbm": {"algorithmic_bytes": alg_bytes,
+                             "achieved": round(alg_bytes / (ms * 1e-3) / 1e9, 1),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s"}},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    pool.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -370,6 +457,9 @@ def main() -> int:
                          "per layer instead of gkv_decode_layer's three)")
     ap.add_argument("--sequential-blocks", action="store_true",
                     help="diagnostics: hand out physical blocks in id order (no shuffle)")
+    ap.add_argument("--qkv-projection", action="store_true",
+                    help="time gkv_qkv_append (QKV projection with the append in its "
+                         "epilogue) on config 2's decode rows instead of the decode step")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="calibration mode: time a plain device copy of this many MiB "
                          "(the reference kernel for scaling rocprofv3 FETCH/WRITE_SIZE)")
@@ -384,6 +474,8 @@ def main() -> int:
     if args.copy_mib:
         return copy_calibration(torch, args)
     gkv = load_gkv()
+    if args.qkv_projection:
+        return run_qkv(torch, gkv, args)
     if args.config == 4:
         return run_prefill(torch, gkv, args)
     dev = torch.device("cuda:0")

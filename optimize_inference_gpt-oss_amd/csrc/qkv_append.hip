@@ -30,11 +30,12 @@
 
 namespace gkv {
 
-constexpr int kGM = 64;      // output rows per workgroup
-constexpr int kGN = 128;     // output columns per workgroup (two heads)
-constexpr int kGK = 64;      // K chunk per pipeline stage
-constexpr int kGStages = 3;  // LDS stages
-constexpr int kGPer = 6;     // direct-to-LDS loads per wave per chunk (2 of x, 4 of W)
+constexpr int kGM = 64; // output rows per workgroup
+// Launch shape: output columns per workgroup (64 or 128: one or two heads),
+// the K chunk of a pipeline stage (32 or 64) and the LDS stages.
+constexpr int kQkvBN = 64;
+constexpr int kQkvBK = 64;
+constexpr int kQkvStages = 3;
 
 struct QkvArgs {
   const uint16_t *x; // bf16 [M][x_stride]
@@ -47,7 +48,20 @@ struct QkvArgs {
   AppendArgs ap; // placement, tables and cache of the append (qkv/q_out/packs unused)
 };
 
+template <int kGN, int kGK, int kGStages>
 __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
+  constexpr int kWN = kGN / 64;                // waves along N (one head each)
+  constexpr int kWM = 4 / kWN;                 // waves along M
+  constexpr int kRT = kGM / 16 / kWM;          // 16-row tiles per wave
+  constexpr int kSPR = kGK / 8;                // 16-byte slots per row of a stage
+  constexpr int kRPC = 64 / kSPR;              // rows per 1 KB direct-to-LDS load
+  constexpr int kXChunks = kGM / kRPC / 4;     // x loads per wave per chunk
+  constexpr int kWChunks = kGN / kRPC / 4;     // W loads per wave per chunk
+  constexpr int kGPer = kXChunks + kWChunks;   // direct-to-LDS loads per wave per chunk
+  // slot swizzle of row r: 8 rows (64-wide chunk) or 4 row groups of 4
+  // (32-wide chunk) see every slot, so the 16 lanes reading one slot column of
+  // 16 rows hit distinct banks
+  auto swz = [](int r) { return kGK == 64 ? (r & 7) : ((r >> 2) & 3); };
   __shared__ __attribute__((aligned(16))) uint16_t x_st[kGStages][kGM * kGK];
   __shared__ __attribute__((aligned(16))) uint16_t w_st[kGStages][kGN * kGK];
   __shared__ int s_pos[kGM], s_off[kGM];
@@ -79,18 +93,18 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
   auto dma = [&](int kc, int st) {
     const int k0 = min(kc, nk - 1) * kGK;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < kXChunks; i++) {
       const int c = wave + 4 * i;
-      const int r = c * 8 + (lane >> 3), slot = lane & 7;
+      const int r = c * kRPC + lane / kSPR, slot = lane % kSPR;
       const int row = min(m0 + r, a.M - 1);
-      dma16(a.x + (int64_t)row * a.x_stride + k0 + 8 * (slot ^ (r & 7)), &x_st[st][c * 512]);
+      dma16(a.x + (int64_t)row * a.x_stride + k0 + 8 * (slot ^ swz(r)), &x_st[st][c * 512]);
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < kWChunks; i++) {
       const int c = wave + 4 * i;
-      const int r = c * 8 + (lane >> 3), slot = lane & 7;
+      const int r = c * kRPC + lane / kSPR, slot = lane % kSPR;
       const int col = min(n0 + r, a.N - 1);
-      dma16(a.w + (int64_t)col * a.K + k0 + 8 * (slot ^ (r & 7)), &w_st[st][c * 512]);
+      dma16(a.w + (int64_t)col * a.K + k0 + 8 * (slot ^ swz(r)), &w_st[st][c * 512]);
     }
   };
 
@@ -157,10 +171,10 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
   };
 
   // ---- main loop
-  const int wm = wave & 1, wn = wave >> 1;
-  f32x4 acc[2][4];
+  const int wm = wave % kWM, wn = wave / kWM;
+  f32x4 acc[kRT][4];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < kRT; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++)
       acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -168,51 +182,54 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
   place_round1();
   dma(0, 0);
   dma(1, 1);
+#pragma unroll
+  for (int p = 2; p < kGStages - 1; p++)
+    dma(p, p);
   int st = 0;
   for (int kc = 0; kc < nk; kc++) {
-    // chunk kc landed (only chunk kc + 1 and the placement loads issued
-    // after chunk kc may still fly); the barrier also frees the stage of
-    // chunk kc - 1 for chunk kc + 2
-    wait_vmcnt<kGPer>();
+    // chunk kc landed (only the next kGStages - 2 chunks and the placement
+    // loads issued after chunk kc may still fly); the barrier also frees the
+    // stage of chunk kc - 1 for chunk kc + kGStages - 1
+    wait_vmcnt<(kGStages - 2) * kGPer>();
     lds_barrier();
     if (kc == 0)
       place_round2(); // round 1 was issued before chunk 0
-    else if (kc == 2)
-      place_round3(); // round 2 was issued in iteration 0, before chunk 2
-    dma(kc + 2, st == 0 ? 2 : st - 1);
+    else if (kc == kGStages - 1)
+      place_round3(); // round 2 was issued in iteration 0, before chunk kGStages - 1
+    dma(kc + kGStages - 1, st == 0 ? kGStages - 1 : st - 1);
     const uint16_t *xs = x_st[st], *ws = w_st[st];
 #pragma unroll
     for (int ks = 0; ks < kGK / 32; ks++) {
-      bf16x8 xo[2], wo[4];
+      bf16x8 xo[kRT], wo[4];
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
-        const int r = 32 * wm + 16 * i + n, s = 4 * ks + kg;
-        xo[i] = *(const bf16x8 *)&xs[r * kGK + 8 * (s ^ (r & 7))];
+      for (int i = 0; i < kRT; i++) {
+        const int r = 16 * kRT * wm + 16 * i + n, s = 4 * ks + kg;
+        xo[i] = *(const bf16x8 *)&xs[r * kGK + 8 * (s ^ swz(r))];
       }
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         const int r = 64 * wn + 16 * j + n, s = 4 * ks + kg;
-        wo[j] = *(const bf16x8 *)&ws[r * kGK + 8 * (s ^ (r & 7))];
+        wo[j] = *(const bf16x8 *)&ws[r * kGK + 8 * (s ^ swz(r))];
       }
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < kRT; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xo[i], wo[j], acc[i][j], 0, 0, 0);
     }
-    st = st == 2 ? 0 : st + 1;
+    st = st == kGStages - 1 ? 0 : st + 1;
   }
   wait_vmcnt<0>(); // every load landed, none still writes LDS
-  // a short K (fewer than 3 chunks) left round 3 for here
-  if (nk <= 2) {
+  // a short K (fewer than kGStages chunks) left round 3 for here
+  if (nk <= kGStages - 1) {
     place_round3();
     wait_vmcnt<0>();
   }
   place_finish();
   __syncthreads();
 
-  // ---- epilogue. acc[i][j][r] is row m0 + 32 wm + 16 i + 4 kg + r, column
-  // n0 + 64 wn + 16 j + n: head hd, dim d = 16 j + n.
+  // ---- epilogue. acc[i][j][r] is row m0 + 16 kRT wm + 16 i + 4 kg + r,
+  // column n0 + 64 wn + 16 j + n: head hd, dim d = 16 j + n.
   const int hd = (n0 >> 6) + wn;
   const int c0 = 64 * hd;
   if (c0 >= a.N)
@@ -222,7 +239,7 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
   for (int j = 0; j < 4; j++)
     bias[j] = a.bias ? a.bias[c0 + 16 * j + n] : 0.0f;
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < kRT; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++)
 #pragma unroll
@@ -230,10 +247,10 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
         acc[i][j][r] += bias[j];
   if (a.out) {
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < kRT; i++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const int m = m0 + 32 * wm + 16 * i + 4 * kg + r;
+        const int m = m0 + 16 * kRT * wm + 16 * i + 4 * kg + r;
         if (m < a.M) {
 #pragma unroll
           for (int j = 0; j < 4; j++)
@@ -247,10 +264,10 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
   const bool is_k = hd < ap.n_q_heads + ap.n_kv_heads;
   const int g = is_k ? hd - ap.n_q_heads : hd - ap.n_q_heads - ap.n_kv_heads;
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < kRT; i++)
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const int lr = 32 * wm + 16 * i + 4 * kg + r; // row within the tile
+      const int lr = 16 * kRT * wm + 16 * i + 4 * kg + r; // row within the tile
       const int off = s_off[lr];
       const int64_t base = s_base[lr] + (int64_t)g * (kBlockTokens * D);
       const bool st_ok = m0 + lr < a.M && off >= 0;
@@ -313,7 +330,7 @@ extern "C" int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64
   const int64_t n_cols = (int64_t)(n_q_heads + 2 * cache.n_kv_heads) * kHeadDim;
   if (n_cols >= INT32_MAX || x_stride < hidden || (qkv_out && out_stride < n_cols))
     return GKV_ERR_ARG;
-  if (hidden % kGK != 0)
+  if (hidden % kQkvBK != 0)
     return GKV_ERR_UNSUPPORTED;
   // 16-byte direct-to-LDS loads of x and W rows
   if (x_stride % 8 != 0 || ((uintptr_t)x | (uintptr_t)w_qkv) % 16 != 0)
@@ -345,7 +362,7 @@ extern "C" int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64
   a.N = (int)n_cols;
   a.K = hidden;
   a.m_blocks = (n_rows + kGM - 1) / kGM;
-  const int n_blocks = (int)((n_cols + kGN - 1) / kGN);
+  const int n_blocks = (int)((n_cols + kQkvBN - 1) / kQkvBN);
   a.xcd_map = n_blocks % 8 == 0;
   const int64_t grid = (int64_t)a.m_blocks * n_blocks;
   if (grid >= INT32_MAX)
@@ -373,7 +390,7 @@ extern "C" int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64
   ap.dev_err = dev_err;
   ap.v_int8 = cache.v_format == GKV_V_INT8;
   ap.vs = (float *)cache.v_scale;
-  hipLaunchKernelGGL(qkv_append_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
-                     a);
+  hipLaunchKernelGGL((qkv_append_kernel<kQkvBN, kQkvBK, kQkvStages>), dim3((unsigned)grid), dim3(256), 0,
+                     (hipStream_t)stream, a);
   return launch_status(__func__);
 }
