@@ -11,17 +11,18 @@
 // gemm_bf16 writes) are stored too when asked: the attention reads Q from
 // them.
 //
-// Work: one workgroup of 4 waves per 64 x 128 output tile (two heads of 64
-// columns), the K dimension in chunks of 64 through a 3-stage LDS pipeline
-// fed by direct-to-LDS loads (16-byte slots XOR-swizzled per row, as in the
-// prefill kernel). Wave (wm, wn) owns rows 32 wm .. +31 and head wn of the
-// tile: 2 x 4 tiles of v_mfma_f32_16x16x32_bf16, so a lane holds dims d and
-// d + 32 of its rows -- both halves of a RoPE pair -- in registers. With the
-// number of column blocks a multiple of 8, the row blocks of one column block
-// run on one XCD (their W tile is read from one L2).
+// Work: one workgroup per kQkvBM x kQkvBN output tile (as built 64 x 64, one
+// head, 4 waves; three workgroups per CU), the K dimension in chunks of 64
+// through a 3-stage LDS pipeline fed by direct-to-LDS loads (16-byte slots
+// XOR-swizzled per row, as in the prefill kernel). Each wave owns 16 rows
+// (kRT row tiles of 16) and one head of the tile: kRT x 4 tiles of
+// v_mfma_f32_16x16x32_bf16, so a lane holds dims d and d + 32 of its rows --
+// both halves of a RoPE pair -- in registers. With the number of column
+// blocks a multiple of 8, the row blocks of one column block run on one XCD
+// (their W tile is read from one L2).
 //
 // Placement of each row (its sequence, position, slot and block) is loaded by
-// wave 0 in three dependent rounds of direct-to-LDS loads spread over the
+// the first waves in three dependent rounds of direct-to-LDS loads spread over the
 // first main-loop iterations, so its round trips overlap the loop instead of
 // adding to it.
 #include "gkv_device.hpp"
@@ -30,9 +31,11 @@
 
 namespace gkv {
 
-constexpr int kGM = 64; // output rows per workgroup
-// Launch shape: output columns per workgroup (64 or 128: one or two heads),
-// the K chunk of a pipeline stage (32 or 64) and the LDS stages.
+// Launch shape: output rows per workgroup (64 or 128), output columns (64 or
+// 128: one or two heads), the K chunk of a pipeline stage (32 or 64), the
+// LDS stages and the waves per workgroup.
+constexpr int kQkvBM = 64;
+constexpr int kQkvWaves = 4;
 constexpr int kQkvBN = 64;
 constexpr int kQkvBK = 64;
 constexpr int kQkvStages = 3;
@@ -48,15 +51,16 @@ struct QkvArgs {
   AppendArgs ap; // placement, tables and cache of the append (qkv/q_out/packs unused)
 };
 
-template <int kGN, int kGK, int kGStages>
-__global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
+template <int kGM, int kGN, int kGK, int kGStages, int kNW>
+__global__ __launch_bounds__(64 * kNW) void qkv_append_kernel(QkvArgs a) {
   constexpr int kWN = kGN / 64;                // waves along N (one head each)
-  constexpr int kWM = 4 / kWN;                 // waves along M
+  constexpr int kWM = kNW / kWN;               // waves along M
   constexpr int kRT = kGM / 16 / kWM;          // 16-row tiles per wave
   constexpr int kSPR = kGK / 8;                // 16-byte slots per row of a stage
   constexpr int kRPC = 64 / kSPR;              // rows per 1 KB direct-to-LDS load
-  constexpr int kXChunks = kGM / kRPC / 4;     // x loads per wave per chunk
-  constexpr int kWChunks = kGN / kRPC / 4;     // W loads per wave per chunk
+  constexpr int kXChunks = kGM / kRPC / kNW;   // x loads per wave per chunk
+  constexpr int kWChunks = kGN / kRPC / kNW;   // W loads per wave per chunk
+  static_assert(kRT >= 1 && kXChunks >= 1 && kWChunks >= 1, "launch shape");
   constexpr int kGPer = kXChunks + kWChunks;   // direct-to-LDS loads per wave per chunk
   // slot swizzle of row r: 8 rows (64-wide chunk) or 4 row groups of 4
   // (32-wide chunk) see every slot, so the 16 lanes reading one slot column of
@@ -94,41 +98,43 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
     const int k0 = min(kc, nk - 1) * kGK;
 #pragma unroll
     for (int i = 0; i < kXChunks; i++) {
-      const int c = wave + 4 * i;
+      const int c = wave + kNW * i;
       const int r = c * kRPC + lane / kSPR, slot = lane % kSPR;
       const int row = min(m0 + r, a.M - 1);
       dma16(a.x + (int64_t)row * a.x_stride + k0 + 8 * (slot ^ swz(r)), &x_st[st][c * 512]);
     }
 #pragma unroll
     for (int i = 0; i < kWChunks; i++) {
-      const int c = wave + 4 * i;
+      const int c = wave + kNW * i;
       const int r = c * kRPC + lane / kSPR, slot = lane % kSPR;
       const int col = min(n0 + r, a.N - 1);
       dma16(a.w + (int64_t)col * a.K + k0 + 8 * (slot ^ swz(r)), &w_st[st][c * 512]);
     }
   };
 
-  // ---- row placement (wave 0, lane t = row m0 + t): round 1 loads the
-  // row's sequence and position, round 2 its sequence length, round 3 its
-  // block id, each a direct-to-LDS load (a register load would be left in
-  // flight across code the compiler schedules freely); rounds 2 and 3 are
-  // issued inside the main loop after waits that cover the round before.
-  const int pr = min(m0 + lane, a.M - 1);
-  const bool place = wave == 0 && appends;
+  // ---- row placement (waves 0 .. kGM/64 - 1; lane t of wave w: row
+  // m0 + 64 w + t): round 1 loads the row's sequence and position, round 2
+  // its sequence length, round 3 its block id, each a direct-to-LDS load (a
+  // register load would be left in flight across code the compiler schedules
+  // freely); rounds 2 and 3 are issued inside the main loop after waits that
+  // cover the round before.
+  const int prl = 64 * wave + lane; // row within the tile
+  const int pr = min(m0 + prl, a.M - 1);
+  const bool place = wave < kGM / 64 && appends;
   const bool need_len = ap.seq_lens && (!ap.row_pos || ap.ring > 0);
   auto place_round1 = [&]() {
     if (!place)
       return;
     if (ap.row_seq)
-      dma4(ap.row_seq + pr, s_seq);
+      dma4(ap.row_seq + pr, s_seq + 64 * wave);
     if (ap.row_pos)
-      dma4(ap.row_pos + pr, s_rpos);
+      dma4(ap.row_pos + pr, s_rpos + 64 * wave);
   };
-  auto row_seq_of = [&]() { return ap.row_seq ? s_seq[lane] : pr; };
+  auto row_seq_of = [&]() { return ap.row_seq ? s_seq[prl] : pr; };
   auto place_round2 = [&]() {
     if (!place || !need_len)
       return;
-    dma4(ap.seq_lens + row_seq_of(), s_len);
+    dma4(ap.seq_lens + row_seq_of(), s_len + 64 * wave);
   };
   int p_slot = 0, p_pos = 0;
   bool p_store = false;
@@ -136,11 +142,11 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
     if (!place)
       return;
     const int seq = row_seq_of();
-    const int len = need_len ? s_len[lane] : 0;
-    const int pos = ap.row_pos ? s_rpos[lane] : len - 1;
+    const int len = need_len ? s_len[prl] : 0;
+    const int pos = ap.row_pos ? s_rpos[prl] : len - 1;
     p_pos = pos;
     p_slot = ap.ring > 0 ? pos % ap.ring : pos;
-    p_store = m0 + lane < a.M && pos >= 0;
+    p_store = m0 + prl < a.M && pos >= 0;
     if (p_store && ap.ring > 0 && ap.seq_lens && pos + ap.ring < len)
       p_store = false; // a later row of this call takes the ring slot
     const int blk = p_slot / kBlockTokens;
@@ -150,14 +156,14 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
       p_store = false;
     }
     // rows that are not stored load entry 0 (any valid address)
-    dma4(ap.table + (p_store ? (int64_t)seq * ap.table_stride + blk : 0), s_id);
+    dma4(ap.table + (p_store ? (int64_t)seq * ap.table_stride + blk : 0), s_id + 64 * wave);
   };
   auto place_finish = [&]() { // after the loop's final wait: every load has landed
-    if (wave != 0)
+    if (wave >= kGM / 64)
       return;
     int64_t base = -1;
     if (place && p_store) {
-      const int id = s_id[lane];
+      const int id = s_id[prl];
       if (id < 0 || id >= ap.num_blocks) {
         if (ap.dev_err)
           atomicOr(ap.dev_err, GKV_DEVERR_BLOCK_ID);
@@ -165,9 +171,9 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
         base = (int64_t)id * ap.n_kv_heads * (kBlockTokens * kHeadDim);
       }
     }
-    s_pos[lane] = max(p_pos, 0);
-    s_off[lane] = base >= 0 ? p_slot % kBlockTokens : -1;
-    s_base[lane] = base;
+    s_pos[prl] = max(p_pos, 0);
+    s_off[prl] = base >= 0 ? p_slot % kBlockTokens : -1;
+    s_base[prl] = base;
   };
 
   // ---- main loop
@@ -361,7 +367,7 @@ extern "C" int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64
   a.M = n_rows;
   a.N = (int)n_cols;
   a.K = hidden;
-  a.m_blocks = (n_rows + kGM - 1) / kGM;
+  a.m_blocks = (n_rows + kQkvBM - 1) / kQkvBM;
   const int n_blocks = (int)((n_cols + kQkvBN - 1) / kQkvBN);
   a.xcd_map = n_blocks % 8 == 0;
   const int64_t grid = (int64_t)a.m_blocks * n_blocks;
@@ -390,7 +396,8 @@ extern "C" int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64
   ap.dev_err = dev_err;
   ap.v_int8 = cache.v_format == GKV_V_INT8;
   ap.vs = (float *)cache.v_scale;
-  hipLaunchKernelGGL((qkv_append_kernel<kQkvBN, kQkvBK, kQkvStages>), dim3((unsigned)grid), dim3(256), 0,
+  hipLaunchKernelGGL((qkv_append_kernel<kQkvBM, kQkvBN, kQkvBK, kQkvStages, kQkvWaves>),
+                     dim3((unsigned)grid), dim3(64 * kQkvWaves), 0,
                      (hipStream_t)stream, a);
   return launch_status(__func__);
 }
