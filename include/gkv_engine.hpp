@@ -64,6 +64,22 @@ inline void rope_kv_bf16(stream_t s, int B, float *qkv, int row_stride, const Pa
         "rope_kv_bf16");
 }
 
+// gemm_bf16 (getp-csrc/kernels/fast_gemm.hpp:888-899) followed by
+// rope_kv_bf16(rotate_q = false), the pair at gpu_engine.hpp:493-496:
+// C = A . W^T + bias into fp32 rows (the Q part left unrotated, as gemm_bf16
+// writes it) and each row's rotated K and its V stored into the layer's paged
+// cache at its position, in one gkv_qkv_append call. N must be
+// (n_q_heads + 2 Hkv) * 64.
+inline void gemm_bf16_rope_kv(stream_t s, const bf16_t *A, int M, const bf16_t *W,
+                              const float *bias, float *C, int N, int K, const PagedBatch &bt,
+                              int n_q_heads, const PagedLayer &layer) {
+  if (N != (n_q_heads + 2 * layer.view.n_kv_heads) * 64)
+    check(GKV_ERR_ARG, "gemm_bf16_rope_kv");
+  check(gkv_qkv_append(s, M, A, K, K, W, bias, n_q_heads, bt.cos_tab, bt.sin_tab, bt.row_pos,
+                       nullptr, bt.seq_lens, layer.view, C, N, bt.dev_err),
+        "gemm_bf16_rope_kv");
+}
+
 // attention_bf16_chunk64 (getp-csrc/kernels/fast_attention.hpp:566-580): one
 // query row per sequence against its cache plus the head's sink, output bf16
 // [B][out_stride]. With q_rotated false the query is rotated on load at

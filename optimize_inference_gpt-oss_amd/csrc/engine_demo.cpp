@@ -5,17 +5,25 @@
 // tables, then per layer rope_kv_bf16(rotate_q = false) and
 // attention_bf16_chunk64 with the query rotated on load.
 //
-//   gkv_engine_demo <in.bin> <out.bin> [fused]
+//   gkv_engine_demo <in.bin> <out.bin> [fused | project]
 // fused: the one-call form rope_kv_attention_bf16 instead of the two calls.
+// project: the qkv rows come from the layer input through the QKV projection
+//   with the append in its epilogue (gemm_bf16_rope_kv, the pair
+//   gemm_bf16 + rope_kv_bf16 of gpu_engine.hpp:493-496), then
+//   attention_bf16_chunk64.
 // in.bin:  int32 P, B, Hq, Hkv, n_layers, window, v_format (gkv_v_format);
 //          fp32 qkv [P][n_layers][B][(Hq+2Hkv)*64];
-//          fp32 sinks [n_layers][Hq]
+//          fp32 sinks [n_layers][Hq];
+//          project only: int32 H; bf16 x [P][n_layers][B][H];
+//          bf16 W [n_layers][(Hq+2Hkv)*64][H]; fp32 bias [n_layers][(Hq+2Hkv)*64]
+//          (the qkv array is then ignored)
 // out.bin: bf16 [P][n_layers][B][Hq*64] attention outputs of every step
 // Layer l is a window layer iff window > 0 and l is even (the pool's rule).
 #include <hip/hip_runtime_api.h>
 
 #include <cstdio>
 #include <cstdlib>
+#include <string>
 #include <vector>
 
 #include "gkv_engine.hpp"
@@ -31,10 +39,11 @@
 
 int main(int argc, char **argv) {
   if (argc != 3 && argc != 4) {
-    fprintf(stderr, "usage: %s in.bin out.bin [fused]\n", argv[0]);
+    fprintf(stderr, "usage: %s in.bin out.bin [fused | project]\n", argv[0]);
     return 2;
   }
-  const bool fused = argc == 4;
+  const bool fused = argc == 4 && std::string(argv[3]) == "fused";
+  const bool project = argc == 4 && std::string(argv[3]) == "project";
   FILE *f = fopen(argv[1], "rb");
   if (!f)
     return 2;
@@ -47,6 +56,20 @@ int main(int argc, char **argv) {
   if (fread(qkv.data(), 4, qkv.size(), f) != qkv.size() ||
       fread(sinks.data(), 4, sinks.size(), f) != sinks.size())
     return 2;
+  int32_t H = 0;
+  std::vector<uint16_t> xs, ws;
+  std::vector<float> bs;
+  if (project) {
+    if (fread(&H, 4, 1, f) != 1 || H <= 0)
+      return 2;
+    xs.resize((size_t)P * NL * B * H);
+    ws.resize((size_t)NL * QKV * H);
+    bs.resize((size_t)NL * QKV);
+    if (fread(xs.data(), 2, xs.size(), f) != xs.size() ||
+        fread(ws.data(), 2, ws.size(), f) != ws.size() ||
+        fread(bs.data(), 4, bs.size(), f) != bs.size())
+      return 2;
+  }
   fclose(f);
 
   gkv_pool_config cfg{};
@@ -87,6 +110,15 @@ int main(int argc, char **argv) {
   HIP_OK(hipMalloc(&d_err, 4));
   HIP_OK(hipMalloc(&d_out, (size_t)B * ATT * 2));
   HIP_OK(hipMalloc(&d_ws, ws_bytes));
+  uint16_t *d_x = nullptr, *d_w = nullptr;
+  float *d_b = nullptr;
+  if (project) {
+    HIP_OK(hipMalloc(&d_x, (size_t)B * H * 2));
+    HIP_OK(hipMalloc(&d_w, ws.size() * 2));
+    HIP_OK(hipMalloc(&d_b, bs.size() * 4));
+    HIP_OK(hipMemcpy(d_w, ws.data(), ws.size() * 2, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(d_b, bs.data(), bs.size() * 4, hipMemcpyHostToDevice));
+  }
   HIP_OK(hipMemcpy(d_sinks, sinks.data(), sinks.size() * 4, hipMemcpyHostToDevice));
   HIP_OK(hipMemcpy(d_cos, cos_h.data(), cos_h.size() * 4, hipMemcpyHostToDevice));
   HIP_OK(hipMemcpy(d_sin, sin_h.data(), sin_h.size() * 4, hipMemcpyHostToDevice));
@@ -112,13 +144,21 @@ int main(int argc, char **argv) {
     HIP_OK(hipMemcpyAsync(d_pos, pos.data(), B * 4, hipMemcpyHostToDevice, s));
     HIP_OK(hipMemcpyAsync(d_lens, lens.data(), B * 4, hipMemcpyHostToDevice, s));
     for (int l = 0; l < NL; l++) {
-      HIP_OK(hipMemcpyAsync(d_qkv, qkv.data() + ((size_t)p * NL + l) * B * QKV,
-                            (size_t)B * QKV * 4, hipMemcpyHostToDevice, s));
-      if (fused) {
-        gkv_engine::rope_kv_attention_bf16(s, B, d_qkv, QKV, layers[l], Hq, d_out, ATT, bt);
-      } else {
-        gkv_engine::rope_kv_bf16(s, B, d_qkv, QKV, bt, Hq, layers[l], /*rotate_q=*/false);
+      if (project) {
+        HIP_OK(hipMemcpyAsync(d_x, xs.data() + ((size_t)p * NL + l) * B * H, (size_t)B * H * 2,
+                              hipMemcpyHostToDevice, s));
+        gkv_engine::gemm_bf16_rope_kv(s, d_x, B, d_w + (size_t)l * QKV * H, d_b + (size_t)l * QKV,
+                                      d_qkv, QKV, H, bt, Hq, layers[l]);
         gkv_engine::attention_bf16_chunk64(s, d_qkv, QKV, layers[l], Hq, d_out, ATT, B, bt);
+      } else {
+        HIP_OK(hipMemcpyAsync(d_qkv, qkv.data() + ((size_t)p * NL + l) * B * QKV,
+                              (size_t)B * QKV * 4, hipMemcpyHostToDevice, s));
+        if (fused) {
+          gkv_engine::rope_kv_attention_bf16(s, B, d_qkv, QKV, layers[l], Hq, d_out, ATT, bt);
+        } else {
+          gkv_engine::rope_kv_bf16(s, B, d_qkv, QKV, bt, Hq, layers[l], /*rotate_q=*/false);
+          gkv_engine::attention_bf16_chunk64(s, d_qkv, QKV, layers[l], Hq, d_out, ATT, B, bt);
+        }
       }
       HIP_OK(hipMemcpyAsync(out.data() + ((size_t)p * NL + l) * B * ATT, d_out,
                             (size_t)B * ATT * 2, hipMemcpyDeviceToHost, s));
@@ -137,7 +177,8 @@ int main(int argc, char **argv) {
   fclose(g);
   gkv_pool_destroy(pool);
   for (void *ptr : {(void *)d_qkv, (void *)d_sinks, (void *)d_cos, (void *)d_sin, (void *)d_pos,
-                    (void *)d_lens, (void *)d_err, (void *)d_out, d_ws})
+                    (void *)d_lens, (void *)d_err, (void *)d_out, d_ws, (void *)d_x, (void *)d_w,
+                    (void *)d_b})
     (void)hipFree(ptr);
   (void)hipStreamDestroy(s);
   printf("engine demo: %d steps x %d layers x %d sequences ok\n", P, NL, B);

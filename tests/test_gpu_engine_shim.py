@@ -4,6 +4,7 @@ build()) calls rope_kv_bf16 + attention_bf16_chunk64 per layer and step over
 the paged pool (one window layer with a wrapping 32-slot ring, one full
 layer). Every step's bf16 output is compared with the CPU oracle, which keeps
 the history by position: max-abs 2e-3 + rel 1e-2, plus bf16 output rounding.
+The "project" form also runs the QKV projection through gemm_bf16_rope_kv.
 """
 import os
 import subprocess
@@ -19,20 +20,45 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 DEMO = os.path.join(ROOT, "optimize_inference_gpt-oss_amd", "gkv_engine_demo")
 
 
-@pytest.mark.parametrize("fused,v_int8", [(False, False), (True, False), (True, True)])
-def test_engine_shim_decode_loop(oracle, cuda, tmp_path, fused, v_int8):
+def _bf16_values(a):
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    return u.view(np.float32)
+
+
+@pytest.mark.parametrize("mode,v_int8", [(None, False), ("fused", False), ("fused", True),
+                                         ("project", False)])
+def test_engine_shim_decode_loop(oracle, cuda, tmp_path, mode, v_int8):
+    """mode None: rope_kv_bf16 + attention_bf16_chunk64; "fused": the one-call
+    rope_kv_attention_bf16; "project": the qkv rows come from the layer input
+    through gemm_bf16_rope_kv (projection with the append in its epilogue),
+    and the oracle's rows from orc_linear (run.cpp matmul + bias)."""
     if not os.path.exists(DEMO):
         pytest.fail("gkv_engine_demo is not built (run __graft_entry__.build())")
     P, B, Hq, Hkv, NL, W = 40, 3, 64, 8, 2, 32
     rng = np.random.default_rng(2024)
-    qkv = (rng.standard_normal((P, NL, B, (Hq + 2 * Hkv) * 64)) * 0.5).astype(np.float32)
+    QKV = (Hq + 2 * Hkv) * 64
+    qkv = (rng.standard_normal((P, NL, B, QKV)) * 0.5).astype(np.float32)
     sinks = rng.standard_normal((NL, Hq)).astype(np.float32)
+    H = 192
+    if mode == "project":
+        x = _bf16_values(rng.standard_normal((P, NL, B, H)))
+        w = _bf16_values(rng.standard_normal((NL, QKV, H)) * 0.04)
+        bias = (rng.standard_normal((NL, QKV)) * 0.1).astype(np.float32)
+        for p in range(P):
+            for l in range(NL):
+                qkv[p, l] = oracle.linear(x[p, l], w[l], bias[l])
     inp, outp = tmp_path / "in.bin", tmp_path / "out.bin"
     with open(inp, "wb") as f:
         np.array([P, B, Hq, Hkv, NL, W, 1 if v_int8 else 0], np.int32).tofile(f)
         qkv.tofile(f)
         sinks.tofile(f)
-    cmd = [DEMO, str(inp), str(outp)] + (["fused"] if fused else [])
+        if mode == "project":
+            np.array([H], np.int32).tofile(f)
+            for a in (x, w):
+                (a.view(np.uint32) >> 16).astype(np.uint16).tofile(f)
+            bias.tofile(f)
+    cmd = [DEMO, str(inp), str(outp)] + ([mode] if mode else [])
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=90)
     assert r.returncode == 0, r.stderr
     got = np.fromfile(outp, np.uint16).reshape(P, NL, B, Hq, 64)
