@@ -84,6 +84,35 @@ def test_append_argument_checks(gkv):
     assert call(args(n=0)) == gkv.GKV_OK                        # nothing to do
 
 
+def test_qkv_append_argument_checks(gkv):
+    L = gkv.lib()
+    fake = 0x1000  # never dereferenced: the checks fail first
+    N = 80 * 64
+    args = lambda **o: dict(dict(n=4, x=fake, x_stride=2880, hidden=2880, w=fake, b=None, hq=64,
+                                 cos=fake, sin=fake, pos=None, seq=None, lens=fake,
+                                 view=_view(gkv), out=fake, out_stride=N, err=None), **o)
+    def call(a):
+        return L.gkv_qkv_append(None, a["n"], a["x"], a["x_stride"], a["hidden"], a["w"], a["b"],
+                                a["hq"], a["cos"], a["sin"], a["pos"], a["seq"], a["lens"],
+                                a["view"], a["out"], a["out_stride"], a["err"])
+    assert call(args(n=-1)) == gkv.GKV_ERR_ARG
+    assert call(args(x=None)) == gkv.GKV_ERR_ARG
+    assert call(args(w=None)) == gkv.GKV_ERR_ARG
+    assert call(args(hq=60)) == gkv.GKV_ERR_ARG                 # not a multiple of Hkv
+    assert call(args(x_stride=2000)) == gkv.GKV_ERR_ARG         # row shorter than hidden
+    assert call(args(out_stride=N - 1)) == gkv.GKV_ERR_ARG      # row shorter than q|k|v
+    assert call(args(hidden=2900, x_stride=2904)) == gkv.GKV_ERR_UNSUPPORTED  # not 64k
+    assert call(args(x_stride=2884)) == gkv.GKV_ERR_ARG         # 16-byte rows
+    assert call(args(x=fake + 2)) == gkv.GKV_ERR_ARG            # 16-byte aligned
+    assert call(args(cos=None)) == gkv.GKV_ERR_ARG              # the append needs the angles
+    assert call(args(lens=None)) == gkv.GKV_ERR_ARG             # no way to find positions
+    assert call(args(view=_view(gkv, ring=100))) == gkv.GKV_ERR_UNSUPPORTED
+    assert call(args(view=_view(gkv, k=None, v=None), out=None)) == gkv.GKV_ERR_ARG  # no output
+    assert call(args(n=0)) == gkv.GKV_OK                         # nothing to do
+    # projection only: no cache, no angles needed
+    assert call(args(n=0, view=_view(gkv, k=None, v=None), cos=None, sin=None)) == gkv.GKV_OK
+
+
 def test_decode_argument_checks(gkv):
     L = gkv.lib()
     fake = 0x1000
