@@ -407,6 +407,11 @@ def run_qkv(torch, gkv, args) -> int:
     flops = 2.0 * B * N * hidden
     tflops = flops / (ms * 1e-3) / 1e12
     alg_bytes = float(B * hidden * 2 + N * hidden * 2 + N * 4 + B * N * 4 + B * Hkv * D * 2 * 2)
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "qkv_append_config2_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
     line = {
         "metric": "QKV projection + KV append throughput (TFLOP/s), config-2 decode rows",
         "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -420,7 +425,7 @@ def run_qkv(torch, gkv, args) -> int:
                    "parallelism": "1 GPU"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
                      "kernel": "qkv_append_kernel", "kernel_us": round(ms * 1e3, 2),
                      "algorithmic_flops": flops,
                      "hbm": {"algorithmic_bytes": alg_bytes,
