@@ -22,7 +22,7 @@
 // (their W tile is read from one L2).
 //
 // Placement of each row (its sequence, position, slot and block) is loaded by
-// the first waves in three dependent rounds of direct-to-LDS loads spread over the
+// the first waves in three dependent hops of direct-to-LDS loads spread over the
 // first main-loop iterations, so its round trips overlap the loop instead of
 // adding to it.
 #include "gkv_device.hpp"
@@ -113,16 +113,16 @@ __global__ __launch_bounds__(64 * kNW) void qkv_append_kernel(QkvArgs a) {
   };
 
   // ---- row placement (waves 0 .. kGM/64 - 1; lane t of wave w: row
-  // m0 + 64 w + t): round 1 loads the row's sequence and position, round 2
-  // its sequence length, round 3 its block id, each a direct-to-LDS load (a
+  // m0 + 64 w + t): hop 1 loads the row's sequence and position, hop 2
+  // its sequence length, hop 3 its block id, each a direct-to-LDS load (a
   // register load would be left in flight across code the compiler schedules
-  // freely); rounds 2 and 3 are issued inside the main loop after waits that
-  // cover the round before.
+  // freely); hops 2 and 3 are issued inside the main loop after waits that
+  // cover the hop before.
   const int prl = 64 * wave + lane; // row within the tile
   const int pr = min(m0 + prl, a.M - 1);
   const bool place = wave < kGM / 64 && appends;
   const bool need_len = ap.seq_lens && (!ap.row_pos || ap.ring > 0);
-  auto place_round1 = [&]() {
+  auto place_hop1 = [&]() {
     if (!place)
       return;
     if (ap.row_seq)
@@ -131,14 +131,14 @@ __global__ __launch_bounds__(64 * kNW) void qkv_append_kernel(QkvArgs a) {
       dma4(ap.row_pos + pr, s_rpos + 64 * wave);
   };
   auto row_seq_of = [&]() { return ap.row_seq ? s_seq[prl] : pr; };
-  auto place_round2 = [&]() {
+  auto place_hop2 = [&]() {
     if (!place || !need_len)
       return;
     dma4(ap.seq_lens + row_seq_of(), s_len + 64 * wave);
   };
   int p_slot = 0, p_pos = 0;
   bool p_store = false;
-  auto place_round3 = [&]() {
+  auto place_hop3 = [&]() {
     if (!place)
       return;
     const int seq = row_seq_of();
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(64 * kNW) void qkv_append_kernel(QkvArgs a) {
     for (int j = 0; j < 4; j++)
       acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  place_round1();
+  place_hop1();
   dma(0, 0);
   dma(1, 1);
 #pragma unroll
@@ -199,9 +199,9 @@ __global__ __launch_bounds__(64 * kNW) void qkv_append_kernel(QkvArgs a) {
     wait_vmcnt<(kGStages - 2) * kGPer>();
     lds_barrier();
     if (kc == 0)
-      place_round2(); // round 1 was issued before chunk 0
+      place_hop2(); // hop 1 was issued before chunk 0
     else if (kc == kGStages - 1)
-      place_round3(); // round 2 was issued in iteration 0, before chunk kGStages - 1
+      place_hop3(); // hop 2 was issued in iteration 0, before chunk kGStages - 1
     dma(kc + kGStages - 1, st == 0 ? kGStages - 1 : st - 1);
     const uint16_t *xs = x_st[st], *ws = w_st[st];
 #pragma unroll
@@ -226,9 +226,9 @@ __global__ __launch_bounds__(64 * kNW) void qkv_append_kernel(QkvArgs a) {
     st = st == kGStages - 1 ? 0 : st + 1;
   }
   wait_vmcnt<0>(); // every load landed, none still writes LDS
-  // a short K (fewer than kGStages chunks) left round 3 for here
+  // a short K (fewer than kGStages chunks) left hop 3 for here
   if (nk <= kGStages - 1) {
-    place_round3();
+    place_hop3();
     wait_vmcnt<0>();
   }
   place_finish();
