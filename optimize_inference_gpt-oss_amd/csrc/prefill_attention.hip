@@ -30,10 +30,11 @@
 // with the sink, and the sink added in the final normalisation, as in the
 // decode kernel. The row sums are fp32 sums of the same fp16 weights.
 //
-// LDS (73 KB, two workgroups per CU): a pipeline of 4 K/V tile stages of 64
-// keys, fed by direct-to-LDS loads 3 tiles ahead (K and V rows as they are in
-// memory, 16-byte slots XOR-swizzled per key row); each tile's V is turned
-// into V^T [64 dims][64 keys + 8 pad] fp16 just before the tile is used.
+// LDS (66 KB, two workgroups per CU): a pipeline of 3 K/V tile stages of 64
+// keys, fed by direct-to-LDS loads 2 tiles ahead (K and V rows as they are in
+// memory, 16-byte slots XOR-swizzled per key row); the V of tile t + 1 is
+// turned into V^T [64 dims][64 keys + 8 pad] fp16 while tile t is computed,
+// into the other of two V^T buffers, so a tile needs one barrier.
 #include "gkv_device.hpp"
 #include "lds_dma.hpp"
 
@@ -43,7 +44,7 @@ constexpr int kQBlock = 32;         // query positions per workgroup
 constexpr int kKTile = 64;          // keys per LDS tile
 constexpr int kVRow = kKTile + 8;   // fp16 per V^T row in LDS
 constexpr float kVScale = 0x1p-10f; // V is staged as fp16 of v * kVScale
-constexpr int kStages = 4;          // K/V tile pipeline depth (tiles held in LDS)
+constexpr int kStages = 3;          // K/V tile pipeline depth (tiles held in LDS)
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 struct PrefillArgs {
@@ -69,12 +70,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   // each 128-byte key row's 16-byte slots XOR-swizzled by key % 8 (slot s of
   // key r holds dims 8 (s ^ (r % 8))), one array per stage so that a read of
   // one stage waits only for that stage's loads; and V^T in fp16 for the tile
-  // being computed. 73 KB: two workgroups per CU.
+  // being computed and the next one. 66 KB: two workgroups per CU.
+  static_assert(kStages == 3, "one array per stage below");
   __shared__ __attribute__((aligned(16))) uint16_t k_st0[kKTile * D], k_st1[kKTile * D],
-      k_st2[kKTile * D], k_st3[kKTile * D];
+      k_st2[kKTile * D];
   __shared__ __attribute__((aligned(16))) uint16_t v_st0[kKTile * D], v_st1[kKTile * D],
-      v_st2[kKTile * D], v_st3[kKTile * D];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[D * kVRow];
+      v_st2[kKTile * D];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2 * D * kVRow];
 
   int id = blockIdx.x;
   const int g = id % a.n_kv_heads;
@@ -106,10 +108,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   // past the prompt clamped, tiles past the last re-read), so the number of
   // loads that follow a tile's is fixed and the wait below is exact.
   auto k_stage = [&](int st) -> uint16_t * {
-    return st == 0 ? k_st0 : st == 1 ? k_st1 : st == 2 ? k_st2 : k_st3;
+    return st == 0 ? k_st0 : st == 1 ? k_st1 : k_st2;
   };
   auto v_stage = [&](int st) -> uint16_t * {
-    return st == 0 ? v_st0 : st == 1 ? v_st1 : st == 2 ? v_st2 : v_st3;
+    return st == 0 ? v_st0 : st == 1 ? v_st1 : v_st2;
   };
   auto dma = [&](int t, int st) {
     const int kt0 = k_lo + t * kKTile;
@@ -134,8 +136,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
     const _Float16 h = (_Float16)(bf16_to_f32((uint16_t)bits16) * kVScale);
     return (uint32_t)__builtin_bit_cast(uint16_t, h);
   };
-  auto convert_v = [&](int st) {
+  auto convert_v = [&](int st, int buf) {
     const uint16_t *vs = v_stage(st);
+    uint16_t *vt_w = v_lds + buf * (D * kVRow);
 #pragma unroll
     for (int i = 0; i < kPieces; i++) {
       const int idx = tid + i * NT;
@@ -147,7 +150,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         const uint32_t wa = x[j >> 1] >> (16 * (j & 1)), wb = y[j >> 1] >> (16 * (j & 1));
-        *(uint32_t *)&v_lds[(4 * pd + j) * kVRow + 2 * pr] =
+        *(uint32_t *)&vt_w[(4 * pd + j) * kVRow + 2 * pr] =
             v_half(wa & 0xffffu) | (v_half(wb & 0xffffu) << 16);
       }
     }
@@ -212,17 +215,19 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
     for (int nn = 0; nn < 4; nn++)
       o[c][nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Tile t in stage st: wait until this wave's loads of tile t have landed
-  // (the loads of the next kStages - 2 tiles may still fly), then the barrier
-  // makes every wave's loads visible and frees the stage of tile t-1, which
-  // takes the loads of tile t + kStages - 1.
+  // Tile t in stage st: wait until this wave's loads of tile t + 1 have
+  // landed (issued one tile ago), then the barrier makes every wave's loads
+  // visible, the V^T of tile t (converted during tile t - 1) complete, and
+  // frees the stage of tile t - 1 and the V^T buffer it used: the stage takes
+  // the loads of tile t + kStages - 1, the buffer the V^T of tile t + 1. One
+  // barrier per tile.
   auto tile = [&](const int t, const int st) {
-    wait_vmcnt<(kStages - 2) * 2 * (8 / NW)>();
+    wait_vmcnt<0>();
     lds_barrier();
     dma(t + kStages - 1, (st + kStages - 1) % kStages);
-    convert_v(st);
-    lds_barrier();
+    convert_v((st + 1) % kStages, (t + 1) & 1);
     const uint16_t *ks = k_stage(st);
+    const uint16_t *vt = v_lds + (t & 1) * (D * kVRow);
     const int kt0 = k_lo + t * kKTile;
 #pragma unroll
     for (int s = 0; s < kKTile / 32; s++) {
@@ -306,7 +311,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
       }
 #pragma unroll
       for (int nn = 0; nn < 4; nn++) {
-        const uint16_t *vrow = &v_lds[(16 * nn + n) * kVRow + 32 * s + 4 * kg];
+        const uint16_t *vrow = &vt[(16 * nn + n) * kVRow + 32 * s + 4 * kg];
         const u32x2 x = *(const u32x2 *)vrow;
         const u32x2 y = *(const u32x2 *)(vrow + 16);
         const f16x8 vop = __builtin_bit_cast(f16x8, u32x4{x[0], x[1], y[0], y[1]});
@@ -316,6 +321,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
       }
     }
   };
+  // tile 0's V^T before the loop (tile 1's loads may still fly)
+  wait_vmcnt<2 * (8 / NW)>();
+  lds_barrier();
+  convert_v(0, 0);
   for (int t = 0; t < n_tiles; t += kStages) {
     tile(t, 0);
 #pragma unroll
