@@ -355,7 +355,7 @@ def run_qkv(torch, gkv, args) -> int:
     library GEMM (torch.mm, bf16) and gkv_kv_append."""
     dev = torch.device("cuda:0")
     cfg = CONFIGS[2]
-    B, Hq, Hkv, hidden = cfg["B"], cfg["Hq"], cfg["Hkv"], 2880
+    B, Hq, Hkv, hidden = args.qkv_rows or cfg["B"], cfg["Hq"], cfg["Hkv"], 2880
     N = (Hq + 2 * Hkv) * D
     rng = np.random.default_rng(args.seed)
     L = rng.integers(cfg["lo"], cfg["hi"] + 1, size=B).astype(np.int32)
@@ -407,19 +407,19 @@ def run_qkv(torch, gkv, args) -> int:
     flops = 2.0 * B * N * hidden
     tflops = flops / (ms * 1e-3) / 1e12
     alg_bytes = float(B * hidden * 2 + N * hidden * 2 + N * 4 + B * N * 4 + B * Hkv * D * 2 * 2)
-    traffic = None
+    traffic = None  # measured for config 2's 512 rows only
     tpath = os.path.join(ROOT, "profiles", "qkv_append_config2_traffic.json")
-    if os.path.exists(tpath):
+    if B == cfg["B"] and os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
     line = {
-        "metric": "QKV projection + KV append throughput (TFLOP/s), config-2 decode rows",
+        "metric": "QKV projection + KV append throughput (TFLOP/s)",
         "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) x, N(0,1)*0.02 W, N(0,1)*0.1 bias, permuted blocks)",
-        "config": {"workload": "gkv_qkv_append on config 2's decode rows (gpt-oss-20b "
-                               "hidden 2880)", "rows": B, "hidden": hidden, "N": N,
+        "config": {"workload": f"gkv_qkv_append on {B} rows at config 2's lengths "
+                               "(gpt-oss-20b hidden 2880)", "rows": B, "hidden": hidden, "N": N,
                    "unfused_ms": {"torch.mm bf16 (library GEMM, bf16 out)": round(lib_ms, 4),
                                   "gkv_kv_append": round(app_ms, 4)},
                    "parallelism": "1 GPU"},
@@ -465,6 +465,9 @@ def main() -> int:
     ap.add_argument("--qkv-projection", action="store_true",
                     help="time gkv_qkv_append (QKV projection with the append in its "
                          "epilogue) on config 2's decode rows instead of the decode step")
+    ap.add_argument("--qkv-rows", type=int, default=0,
+                    help="rows of the --qkv-projection run (default: config 2's 512 decode rows; "
+                         "config 4's prompts hold 19024)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="calibration mode: time a plain device copy of this many MiB "
                          "(the reference kernel for scaling rocprofv3 FETCH/WRITE_SIZE)")

@@ -31,14 +31,19 @@
 
 namespace gkv {
 
-// Launch shape: output rows per workgroup (64 or 128), output columns (64 or
+// Launch shapes: output rows per workgroup (64 or 128), output columns (64 or
 // 128: one or two heads), the K chunk of a pipeline stage (32 or 64), the
-// LDS stages and the waves per workgroup.
+// LDS stages and the waves per workgroup. Few rows (a decode step): 64 x 64
+// tiles, three workgroups per CU, enough of them to fill the GPU. Many rows
+// (prompts): 128 x 128 tiles with 8 waves and 2 stages (two workgroups per
+// CU), four times the reuse of each loaded byte.
 constexpr int kQkvBM = 64;
 constexpr int kQkvWaves = 4;
 constexpr int kQkvBN = 64;
 constexpr int kQkvBK = 64;
 constexpr int kQkvStages = 3;
+constexpr int kQkvBigRows = 2048; // from this many rows on, the large tiles
+constexpr int kQkvBigBM = 128, kQkvBigBN = 128, kQkvBigWaves = 8, kQkvBigStages = 2;
 
 struct QkvArgs {
   const uint16_t *x; // bf16 [M][x_stride]
@@ -367,8 +372,10 @@ extern "C" int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64
   a.M = n_rows;
   a.N = (int)n_cols;
   a.K = hidden;
-  a.m_blocks = (n_rows + kQkvBM - 1) / kQkvBM;
-  const int n_blocks = (int)((n_cols + kQkvBN - 1) / kQkvBN);
+  const bool big = n_rows >= kQkvBigRows;
+  const int bm = big ? kQkvBigBM : kQkvBM, bn = big ? kQkvBigBN : kQkvBN;
+  a.m_blocks = (n_rows + bm - 1) / bm;
+  const int n_blocks = (int)((n_cols + bn - 1) / bn);
   a.xcd_map = n_blocks % 8 == 0;
   const int64_t grid = (int64_t)a.m_blocks * n_blocks;
   if (grid >= INT32_MAX)
@@ -396,8 +403,12 @@ extern "C" int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64
   ap.dev_err = dev_err;
   ap.v_int8 = cache.v_format == GKV_V_INT8;
   ap.vs = (float *)cache.v_scale;
-  hipLaunchKernelGGL((qkv_append_kernel<kQkvBM, kQkvBN, kQkvBK, kQkvStages, kQkvWaves>),
-                     dim3((unsigned)grid), dim3(64 * kQkvWaves), 0,
-                     (hipStream_t)stream, a);
+  if (big)
+    hipLaunchKernelGGL(
+        (qkv_append_kernel<kQkvBigBM, kQkvBigBN, kQkvBK, kQkvBigStages, kQkvBigWaves>),
+        dim3((unsigned)grid), dim3(64 * kQkvBigWaves), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL((qkv_append_kernel<kQkvBM, kQkvBN, kQkvBK, kQkvStages, kQkvWaves>),
+                       dim3((unsigned)grid), dim3(64 * kQkvWaves), 0, (hipStream_t)stream, a);
   return launch_status(__func__);
 }

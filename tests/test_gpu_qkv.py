@@ -204,6 +204,18 @@ def test_odd_head_count_and_ragged_rows(oracle, gkv, cuda):
     check_cache(case, res, oracle)
 
 
+def test_many_rows_large_tiles(oracle, gkv, cuda):
+    """2,000+ rows take the 128 x 128 tiles: prompt rows with a ragged last
+    row block and a ring window."""
+    import torch
+    case = QkvCase(16, 8, 2, 256, prompts=[700, 513, 900, 1], window=128)
+    assert case.M >= 2048
+    res = run(case, gkv, torch, cuda)
+    assert res["err"] == 0
+    check_projection(case, res, oracle)
+    check_cache(case, res, oracle)
+
+
 def test_projection_only(oracle, gkv, cuda):
     import torch
     case = QkvCase(14, 64, 8, 2880, lens=np.full(33, 5))
