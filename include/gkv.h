@@ -171,7 +171,7 @@ size_t gkv_decode_workspace_bytes(int32_t B, int32_t n_kv_heads, int32_t max_seq
  *   sinks     fp32 [Hq]
  *   split_tokens  0: balanced (the total is cut into equal ranges, one per
  *             workgroup the GPU holds at once); > 0: ranges of this many tokens
- *             (a multiple of 32, at most 4096)
+ *             (a multiple of 32, at most 16384)
  *   max_seq_len   host upper bound of seq_lens (sizes the grid)
  *   out       [B][out_stride] of out_dtype, heads at h*64
  * Launches gkv_decode_prepare, gkv_decode_split and gkv_decode_combine. */

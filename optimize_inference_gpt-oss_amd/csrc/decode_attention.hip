@@ -74,11 +74,9 @@ constexpr int kMlStride = 16;          // floats of (m, l) per partial: 8 heads 
 constexpr int kPartFloats = kCols * kHeadDim;
 constexpr int kMaxWorkgroups = 2048;   // split workgroups per launch (workspace bound)
 constexpr int kPlanHeader = 4;         // ints: T, S, workgroups used, unused
-constexpr int kIdRegs = 4;             // block-id registers per wave: ranges of <= 4096 tokens
-constexpr int kMaxRange = kIdRegs * 64 * kBlockTokens;
-constexpr int kInfoRegs = kMaxRange / kStep / 64; // step-record registers
-constexpr int kIdSlab = kIdRegs * 64;     // block ids per range (its slab in the workspace)
-constexpr int kInfoSlab = kInfoRegs * 64; // step records per range
+constexpr int kMaxRange = 16384;       // tokens per range (its ids and records sit in LDS)
+constexpr int kIdSlab = kMaxRange / kBlockTokens; // block ids per range (its slab in the workspace)
+constexpr int kInfoSlab = kMaxRange / kStep;      // step records per range
 constexpr int kSplitWaves = 4;         // split kernel: one wave per SIMD
 constexpr int kSplitThreads = 64 * kSplitWaves;
 constexpr int kPrepThreads = 1024;
@@ -370,17 +368,23 @@ void decode_split_kernel(DecodeArgs a) {
   constexpr int D = kHeadDim;
   const int w_id = blockIdx.x;
   const int lane = threadIdx.x & 63;
-  // Block ids and step records of the range, one per lane per register. The
+  // Block ids and step records of the range, staged in LDS by the whole
+  // workgroup (the waves stream the same range for different kv heads). The
   // range's slab needs no plan to be found, so these loads go out with the
   // plan's; entries past the range's steps are never read.
-  int tv[kIdRegs], ti[kInfoRegs];
-#pragma unroll
-  for (int i = 0; i < kIdRegs; i++)
-    tv[i] = a.flat[w_id * kIdSlab + 64 * i + lane];
-#pragma unroll
-  for (int i = 0; i < kInfoRegs; i++)
-    ti[i] = a.steps[w_id * kInfoSlab + 64 * i + lane];
+  __shared__ int2 s_ids[kIdSlab / 2]; // the two block ids of each step
+  __shared__ int s_rec[kInfoSlab];
+  {
+    const int4 *src = (const int4 *)(a.flat + (int64_t)w_id * kIdSlab);
+    const int4 *srec = (const int4 *)(a.steps + (int64_t)w_id * kInfoSlab);
+    int4 *dst = (int4 *)s_ids, *drec = (int4 *)s_rec;
+    for (int i = threadIdx.x; i < kIdSlab / 4; i += blockDim.x)
+      dst[i] = src[i];
+    for (int i = threadIdx.x; i < kInfoSlab / 4; i += blockDim.x)
+      drec[i] = srec[i];
+  }
   const int T = a.plan[0], S = a.plan[1];
+  __syncthreads();
   const int rs = w_id * S;
   if (rs >= T)
     return;
@@ -401,15 +405,6 @@ void decode_split_kernel(DecodeArgs a) {
   const size_t head_bytes = (size_t)kBlockTokens * D * 2;               // 2 KB
   const uint32_t vq_off = (uint32_t)(col * 4 + kg) * 16;                 // int8 V piece
 
-
-  auto pick = [&](const int *regs, int nregs, int j) -> int {
-    const int w = j >> 6, l = j & 63;
-    int v = __builtin_amdgcn_readlane(regs[0], l);
-    for (int i = 1; i < nregs; i++)
-      if (w == i)
-        v = __builtin_amdgcn_readlane(regs[i], l);
-    return v;
-  };
 
   // One wave per SIMD. Wave wv takes kv heads wv and wv + n_waves (at most two
   // passes over the range: Hkv <= 8 and n_waves = min(4, Hkv)). The passes form
@@ -434,8 +429,9 @@ void decode_split_kernel(DecodeArgs a) {
     const int pass = v >= n_steps ? 1 : 0;
     const int step = v - pass * n_steps;
     const int g = wv + pass * n_waves;
-    int p0 = pick(tv, kIdRegs, 2 * step), p1 = pick(tv, kIdRegs, 2 * step + 1);
-    rc = pick(ti, kInfoRegs, step);
+    const int2 ids = s_ids[step];
+    int p0 = uniform(ids.x), p1 = uniform(ids.y);
+    rc = uniform(s_rec[step]);
     // a bad id masks its block like padding (bit jt per block)
     bb = (p0 == kBadBlock ? 1 : 0) | (p1 == kBadBlock ? 2 : 0) | (pass << 2);
     p0 = max(p0, 0);

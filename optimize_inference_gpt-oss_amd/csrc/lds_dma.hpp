@@ -41,6 +41,7 @@ __device__ __forceinline__ void dma16(const void *src, void *l_base) {
   uint32_t saved;
   asm volatile("s_mov_b32 %0, m0\n\t"
                "s_mov_b32 m0, %2\n\t"
+               "s_nop 0\n\t" // one wait state between an SALU write of M0 and an LDS-DMA load
                "global_load_lds_dwordx4 %1, off\n\t"
                "s_mov_b32 m0, %0" // M0 as the compiler left it
                : "=&s"(saved)
@@ -54,6 +55,7 @@ __device__ __forceinline__ void dma4(const void *src, void *l_base) {
   uint32_t saved;
   asm volatile("s_mov_b32 %0, m0\n\t"
                "s_mov_b32 m0, %2\n\t"
+               "s_nop 0\n\t"
                "global_load_lds_dword %1, off\n\t"
                "s_mov_b32 m0, %0"
                : "=&s"(saved)

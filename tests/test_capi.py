@@ -141,15 +141,15 @@ def test_decode_argument_checks(gkv):
 
 
 def test_workspace_formula(gkv):
-    # plan (header + prefix sums), block ids (256 per range) and step records
-    # (128 per range) for up to 2048 ranges, query operands (2 KB per sequence
+    # plan (header + prefix sums), block ids (1024 per range) and step records
+    # (512 per range: ranges of up to 16384 tokens) for up to 2048 ranges, query operands (2 KB per sequence
     # and kv head), each 256-byte aligned, then (B + 2048) partials of 8 heads
     # x (64 + 2) floats per kv head
     def a256(x):
         return (x + 255) // 256 * 256
 
     B, hkv = 512, 8
-    fixed = a256((4 + B + 1) * 4) + a256(2048 * 256 * 4) + a256(2048 * 128 * 4)
+    fixed = a256((4 + B + 1) * 4) + a256(2048 * 1024 * 4) + a256(2048 * 512 * 4)
     fixed += a256(B * hkv * 2048)
     assert gkv.workspace_bytes(B, hkv, 2049) == fixed + (B + 2048) * hkv * (512 + 16) * 4
     # a window layer bounds the stream by the window
