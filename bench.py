@@ -460,6 +460,10 @@ def main() -> int:
     ap.add_argument("--separate-append", action="store_true",
                     help="append with gkv_kv_append, then gkv_decode_attention (four launches "
                          "per layer instead of gkv_decode_layer's three)")
+    ap.add_argument("--staged", action="store_true",
+                    help="the staged launches: append fused with the prepare launch (plan, "
+                         "block ids, query operands), then the split reading the plan, then the "
+                         "combine, instead of the one-launch split that plans in its prologue")
     ap.add_argument("--sequential-blocks", action="store_true",
                     help="diagnostics: hand out physical blocks in id order (no shuffle)")
     ap.add_argument("--qkv-projection", action="store_true",
@@ -537,11 +541,17 @@ def main() -> int:
     ev = {}
 
     # A step: per layer, the append of every sequence's new token and the
-    # attention. Default: gkv_decode_layer's three launches (append fused with
-    # the prepare launch, split, combine); --separate-append: gkv_kv_append then
-    # gkv_decode_attention's three launches.
-    stages = ("append", "prepare", "split", "combine") if args.separate_append else \
-        ("append+prepare", "split", "combine")
+    # attention. Default: gkv_decode_layer's two launches (the split, which
+    # plans, prepares the queries and appends in its prologue, then the
+    # combine); --staged: the append fused with a separate prepare launch, then
+    # split and combine; --separate-append: gkv_kv_append, then the staged
+    # prepare, split and combine.
+    if args.separate_append:
+        stages = ("append", "prepare", "split", "combine")
+    elif args.staged:
+        stages = ("append+prepare", "split", "combine")
+    else:
+        stages = ("append+split", "combine")
 
     def step(record: bool):
         for li, layer in enumerate(layers):
@@ -554,7 +564,8 @@ def main() -> int:
                     gkv.kv_append(layer.qkv, Hq, cos_d, sin_d, pos_d, layer.view,
                                   seq_lens=lens_d, dev_err=err_d, stream=stream)
                     continue
-                api = {"append+prepare": "layer_prepare"}.get(stage, stage)
+                api = {"append+prepare": "layer_prepare",
+                       "append+split": "layer_split"}.get(stage, stage)
                 gkv.decode_attention(layer.qkv, lens_d, max_len, layer.view, layer.sinks,
                                      layer.out, window=layer.window, cos_tab=cos_d,
                                      sin_tab=sin_d, split_tokens=args.split_tokens, workspace=ws,
@@ -592,7 +603,7 @@ def main() -> int:
         stage_ms += [np.mean([e[i].elapsed_time(e[i + 1]) for e in lst]) for i in range(n_st)]
     # dominant kernel: the split kernel of the full-attention layers (or of the
     # window layers when there are no full ones)
-    isp = stages.index("split")
+    isp = stages.index("split" if "split" in stages else "append+split")
     full = [i for i, l in enumerate(layers) if not l.window] or list(range(len(layers)))
     dom_ms = float(np.mean([np.mean([e[isp].elapsed_time(e[isp + 1]) for e in ev[i]])
                             for i in full]))
@@ -643,7 +654,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "decode_split_kernel",
+            "kernel": "decode_fused_kernel" if stages[0] == "append+split" else
+                      "decode_split_kernel",
             "kernel_us": round(dom_ms * 1e3, 2),
             "algorithmic_bytes": dom_bytes,
         },

@@ -222,6 +222,12 @@ int gkv_decode_layer(void *stream, int32_t B, int32_t n_q_heads, const float *qk
                      int32_t window, const float *sinks, int32_t split_tokens, void *workspace,
                      size_t workspace_bytes, void *out, int64_t out_stride, int32_t out_dtype,
                      uint32_t *dev_err);
+int gkv_decode_layer_split(void *stream, int32_t B, int32_t n_q_heads, const float *qkv,
+                           int64_t row_stride, const float *cos_tab, const float *sin_tab,
+                           const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,
+                           int32_t window, const float *sinks, int32_t split_tokens,
+                           void *workspace, size_t workspace_bytes, void *out,
+                           int64_t out_stride, int32_t out_dtype, uint32_t *dev_err);
 int gkv_decode_layer_prepare(void *stream, int32_t B, int32_t n_q_heads, const float *qkv,
                              int64_t row_stride, const float *cos_tab, const float *sin_tab,
                              const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,

@@ -57,6 +57,7 @@
 // unconditional (indices are clamped), so the compiler's wait counts are
 // exact and a step never waits for the prefetches issued after it.
 #include "kv_append.hpp"
+#include "lds_dma.hpp"
 
 #include <algorithm>
 #include <cstdlib>
@@ -361,36 +362,19 @@ __global__ __launch_bounds__(kPrepThreads) void decode_layer_prep_kernel(DecodeA
 // ---- split ----------------------------------------------------------------------
 
 // R: depth of the register ring of loaded steps (R - 1 steps in flight ahead
-// of the one being computed).
-template <int R, bool VQ>
-__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(1)))
-void decode_split_kernel(DecodeArgs a) {
+// of the one being computed). Streams range w_id (n_steps steps of 32 tokens)
+// for this wave's kv heads: s_ids holds the two block ids of every step, s_rec
+// its step record (both in LDS, filled by the caller).
+// RAWQ: the ring carries the raw query (fp32, the 16 dims of this lane's
+// column) and the RoPE angles of the sequence's last position (s_len: the
+// sequences' lengths, in LDS), rotated, scaled and split into the operand
+// pieces when the segment opens; otherwise the ring carries the operand
+// pieces prepared by the prepare launch (a.qops).
+template <int R, bool VQ, bool RAWQ>
+__device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, const int2 *s_ids,
+                                             const int *s_rec, const int *s_len, int n_steps) {
   constexpr int D = kHeadDim;
-  const int w_id = blockIdx.x;
   const int lane = threadIdx.x & 63;
-  // Block ids and step records of the range, staged in LDS by the whole
-  // workgroup (the waves stream the same range for different kv heads). The
-  // range's slab needs no plan to be found, so these loads go out with the
-  // plan's; entries past the range's steps are never read.
-  __shared__ int2 s_ids[kIdSlab / 2]; // the two block ids of each step
-  __shared__ int s_rec[kInfoSlab];
-  {
-    const int4 *src = (const int4 *)(a.flat + (int64_t)w_id * kIdSlab);
-    const int4 *srec = (const int4 *)(a.steps + (int64_t)w_id * kInfoSlab);
-    int4 *dst = (int4 *)s_ids, *drec = (int4 *)s_rec;
-    for (int i = threadIdx.x; i < kIdSlab / 4; i += blockDim.x)
-      dst[i] = src[i];
-    for (int i = threadIdx.x; i < kInfoSlab / 4; i += blockDim.x)
-      drec[i] = srec[i];
-  }
-  const int T = a.plan[0], S = a.plan[1];
-  __syncthreads();
-  const int rs = w_id * S;
-  if (rs >= T)
-    return;
-  const int re = min(rs + S, T);
-  const int n_steps = (re - rs) / kStep; // every sequence is padded to whole steps
-
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // wave-uniform
   const int n_waves = blockDim.x >> 6;
   const int col = lane & 15, kg = lane >> 4;
@@ -422,9 +406,11 @@ void decode_split_kernel(DecodeArgs a) {
   // Ring slot: K (4 x 16 B per lane), V (4 x 16 B), the query operands
   // (2 x 16 B; loaded only for a step that opens a segment), the step record,
   // and the bad-block bits | pass << 2.
-  u32x4 kbuf[R][4], vbuf[R][4], qbuf[R][2];
+  constexpr int QN = RAWQ ? 8 : 2; // 16-byte pieces of query data per ring slot
+  u32x4 kbuf[R][4], vbuf[R][4], qbuf[R][QN];
   int rec[R], badb[R];
-  auto load_step = [&](int v, u32x4 (&kr)[4], u32x4 (&vr)[4], u32x4 (&qr)[2], int &rc,
+  const int hq_lane = head_ok ? head : 0; // query head of this lane's column, within the group
+  auto load_step = [&](int v, u32x4 (&kr)[4], u32x4 (&vr)[4], u32x4 (&qr)[QN], int &rc,
                        int &bb) {
     const int pass = v >= n_steps ? 1 : 0;
     const int step = v - pass * n_steps;
@@ -470,10 +456,31 @@ void decode_split_kernel(DecodeArgs a) {
         vr[2 * h + 1] = u32x4{x[2], x[3], y[2], y[3]};
       }
     }
-    if ((rc & 0x80) || step == 0) { // the step opens a segment: its query operands
-      const u32x4 *qs = a.qops + (((int64_t)(rc >> 8) * a.n_kv_heads + g) * 64 + lane) * 2;
-      qr[0] = qs[0];
-      qr[1] = qs[1];
+    if ((rc & 0x80) || step == 0) { // the step opens a segment: its query
+      const int b = rc >> 8;
+      if (RAWQ) {
+        // dims 8kg .. 8kg+7 and 32+8kg .. +7 of the column's query head, and
+        // the angles of those pairs at the sequence's last position
+        const u32x4 *qp = (const u32x4 *)(a.q + (int64_t)b * a.q_stride +
+                                          (g * a.G + hq_lane) * D + 8 * kg);
+        qr[0] = qp[0];
+        qr[1] = qp[1];
+        qr[2] = qp[8];
+        qr[3] = qp[9];
+        if (a.cos_tab) {
+          const int64_t pos = max(s_len[b] - 1, 0);
+          const u32x4 *cp = (const u32x4 *)(a.cos_tab + pos * (D / 2) + 8 * kg);
+          const u32x4 *sp = (const u32x4 *)(a.sin_tab + pos * (D / 2) + 8 * kg);
+          qr[4] = cp[0];
+          qr[5] = cp[1];
+          qr[6] = sp[0];
+          qr[7] = sp[1];
+        }
+      } else {
+        const u32x4 *qs = a.qops + (((int64_t)b * a.n_kv_heads + g) * 64 + lane) * 2;
+        qr[0] = qs[0];
+        qr[1] = qs[1];
+      }
     }
   };
 
@@ -540,7 +547,7 @@ void decode_split_kernel(DecodeArgs a) {
     }
   };
 
-  auto compute_step = [&](u32x4 (&kr)[4], u32x4 (&vr)[4], u32x4 (&qr)[2], int rc, int bb,
+  auto compute_step = [&](u32x4 (&kr)[4], u32x4 (&vr)[4], u32x4 (&qr)[QN], int rc, int bb,
                           bool in_range) {
     const int pass = bb >> 2;
     const int key = (rc >> 8) | (pass << 16);
@@ -558,8 +565,37 @@ void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
       for (int nn = 0; nn < 4; nn++)
         o[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      qcur[0] = qr[0];
-      qcur[1] = qr[1];
+      if (RAWQ) {
+        // RoPE at the last position (as the append rotates K), the scale
+        // 1/sqrt(64) and log2(e) (exp -> exp2), then the bf16 pieces
+        float qa[8], qb[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          qa[i] = __uint_as_float(qr[i >> 2][i & 3]);
+          qb[i] = __uint_as_float(qr[2 + (i >> 2)][i & 3]);
+        }
+        if (a.cos_tab) {
+#pragma unroll
+          for (int i = 0; i < 8; i++) {
+            const float x1 = qa[i], x2 = qb[i];
+            const float c = __uint_as_float(qr[4 + (i >> 2)][i & 3]);
+            const float sn = __uint_as_float(qr[6 + (i >> 2)][i & 3]);
+            qa[i] = rope_first(x1, x2, c, sn);
+            qb[i] = rope_second(x1, x2, c, sn);
+          }
+        }
+        const float qscale = head_ok ? 0.125f * kLog2e : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          qa[i] *= qscale;
+          qb[i] *= qscale;
+        }
+        qcur[0] = __builtin_bit_cast(u32x4, pack_pieces(qa, lo));
+        qcur[1] = __builtin_bit_cast(u32x4, pack_pieces(qb, lo));
+      } else {
+        qcur[0] = qr[0];
+        qcur[1] = qr[1];
+      }
     }
     if (in_range)
       cur_ends = (rc & 0x40) != 0;
@@ -670,6 +706,215 @@ void decode_split_kernel(DecodeArgs a) {
   flush();
 }
 
+// The split launch of the staged path: the plan, block ids and step records
+// come from the prepare launch through the workspace.
+template <int R, bool VQ>
+__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(1)))
+void decode_split_kernel(DecodeArgs a) {
+  const int w_id = blockIdx.x;
+  // Block ids and step records of the range, staged in LDS by the whole
+  // workgroup (the waves stream the same range for different kv heads). The
+  // range's slab needs no plan to be found, so these loads go out with the
+  // plan's; entries past the range's steps are never read.
+  __shared__ int2 s_ids[kIdSlab / 2]; // the two block ids of each step
+  __shared__ int s_rec[kInfoSlab];
+  {
+    const int4 *src = (const int4 *)(a.flat + (int64_t)w_id * kIdSlab);
+    const int4 *srec = (const int4 *)(a.steps + (int64_t)w_id * kInfoSlab);
+    int4 *dst = (int4 *)s_ids, *drec = (int4 *)s_rec;
+    for (int i = threadIdx.x; i < kIdSlab / 4; i += blockDim.x)
+      dst[i] = src[i];
+    for (int i = threadIdx.x; i < kInfoSlab / 4; i += blockDim.x)
+      drec[i] = srec[i];
+  }
+  const int T = a.plan[0], S = a.plan[1];
+  __syncthreads();
+  const int rs = w_id * S;
+  if (rs >= T)
+    return;
+  const int re = min(rs + S, T);
+  stream_range<R, VQ, false>(a, w_id, s_ids, s_rec, nullptr, (re - rs) / kStep);
+}
+
+// ---- fused: plan, append and split in one launch --------------------------------
+
+constexpr int kStepsPerThread = kInfoSlab / 64; // record-building steps per thread (>= 64 threads)
+
+// One launch per decode layer before the combine. Every workgroup repeats the
+// plan: the prefix sums of the padded lengths, in LDS (the lengths are 4
+// bytes per sequence). It then builds the step records and block ids of its
+// own range only, appends the new tokens that fall in its range (one wave per
+// token, all kv heads) and streams the range, the query of each segment
+// coming raw through the load ring. The appends' stores complete before the
+// workgroup barrier that precedes the stream, so every wave of the workgroup
+// reads the new tokens back; no other workgroup reads them (each step of the
+// stream belongs to one range). Workgroup 0 publishes the plan for the
+// combine.
+template <int R, bool VQ>
+__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(1)))
+void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
+  __shared__ int s_cu[kMaxBatch + 1];
+  __shared__ int s_len[kMaxBatch];
+  __shared__ int2 s_ids[kIdSlab / 2];
+  __shared__ int s_rec[kInfoSlab];
+  __shared__ int s_ab[kInfoSlab]; // sequences whose new token lies in the range
+  __shared__ int s_wave[kSplitWaves];
+  __shared__ int s_na;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nt = blockDim.x, B = a.B;
+  const int n_waves = nt >> 6;
+  const int w_id = blockIdx.x;
+
+  // Lengths and padded lengths into LDS (coalesced loads), then the prefix
+  // sums in place: thread t scans sequences t*per .. t*per+per-1.
+  bool any_over = false;
+  for (int b = t; b < B; b += nt) {
+    const int L = a.seq_lens[b];
+    int n = a.window > 0 ? min(L, a.window) : L;
+    const int cap = min(a.table_stride * kBlockTokens, a.max_len);
+    any_over |= n > cap;
+    n = max(min(n, cap), 0);
+    s_len[b] = L;
+    s_cu[b] = pad_step(n);
+  }
+  if (t == 0)
+    s_na = 0;
+  __syncthreads();
+  const int per = (B + nt - 1) / nt;
+  const int b0 = min(t * per, B), b1 = min(b0 + per, B);
+  int local = 0;
+  for (int b = b0; b < b1; b++)
+    local += s_cu[b];
+  int incl = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int v = __shfl_up(incl, off, 64);
+    if (lane >= off)
+      incl += v;
+  }
+  if (lane == 63)
+    s_wave[wave] = incl;
+  __syncthreads();
+  int before = 0, total = 0;
+  for (int w = 0; w < n_waves; w++) {
+    const int v = s_wave[w];
+    before += w < wave ? v : 0;
+    total += v;
+  }
+  int run = before + incl - local;
+  for (int b = b0; b < b1; b++) {
+    const int v = s_cu[b];
+    s_cu[b] = run;
+    run += v;
+  }
+  if (t == 0)
+    s_cu[B] = total;
+  __syncthreads();
+  const int T = s_cu[B];
+  const int S = a.fixed_S > 0 ? a.fixed_S : max(kStep, pad_step((T + a.n_wg - 1) / a.n_wg));
+  if (w_id == 0) {
+    int32_t *cu = a.plan + kPlanHeader;
+    for (int b = t; b <= B; b += nt)
+      cu[b] = s_cu[b];
+    if (t == 0) {
+      a.plan[0] = T;
+      a.plan[1] = S;
+      a.plan[2] = min(a.n_wg, (T + S - 1) / S);
+    }
+    if (any_over && a.dev_err)
+      atomicOr(a.dev_err, GKV_DEVERR_LENGTH);
+  }
+  const int rs = w_id * S;
+  if (rs >= T)
+    return;
+  const int re = min(rs + S, T);
+  const int n_steps = (re - rs) / kStep;
+
+  // Step records and block ids of the range. The table loads go out first;
+  // the list of new tokens in the range is published (LDS barrier, which does
+  // not wait for them) and the appends start while they are in flight.
+  int id0[kStepsPerThread], id1[kStepsPerThread], rcd[kStepsPerThread];
+#pragma unroll
+  for (int k = 0; k < kStepsPerThread; k++) {
+    const int i = t + k * nt;
+    id0[k] = id1[k] = kPadBlock;
+    rcd[k] = 0;
+    if (i < n_steps) {
+      const int tok = rs + i * kStep;
+      int lo = 0, hi = B - 1; // the sequence holding the step: last b with cu[b] <= tok
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_cu[mid] <= tok)
+          lo = mid;
+        else
+          hi = mid - 1;
+      }
+      const int b = lo;
+      const int off = tok - s_cu[b];
+      const int L = s_len[b];
+      int n = a.window > 0 ? min(L, a.window) : L;
+      n = max(min(n, min(a.table_stride * kBlockTokens, a.max_len)), 0);
+      const int32_t *row = a.table + (int64_t)b * a.table_stride + off / kBlockTokens;
+      if (off < n)
+        id0[k] = row[0];
+      if (off + kBlockTokens < n)
+        id1[k] = row[1];
+      rcd[k] = step_record(b, off == 0, tok + kStep == s_cu[b + 1], min(max(n - off, 0), kStep));
+      if (append) {
+        // the new token's slot in the sequence's stream (position L - 1, or
+        // its ring slot)
+        const int slot = a.window > 0 ? (L - 1) % a.window : L - 1;
+        if (L >= 1 && slot < n && slot >= off && slot < off + kStep)
+          s_ab[atomicAdd(&s_na, 1)] = b;
+      }
+    }
+  }
+  lds_barrier();
+
+  // The appends: one wave per new token, every kv head.
+  const int na = s_na;
+  for (int j = wave; j < na; j += n_waves) {
+    const int b = s_ab[j];
+    append_row(ap, b, lane, 0, 1, nullptr, s_len[b] - 1);
+  }
+
+  bool any_bad = false;
+#pragma unroll
+  for (int k = 0; k < kStepsPerThread; k++) {
+    const int i = t + k * nt;
+    if (i < n_steps) {
+      int x = id0[k], y = id1[k];
+      if (x != kPadBlock && (x < 0 || x >= a.num_blocks)) {
+        x = kBadBlock;
+        any_bad = true;
+      }
+      if (y != kPadBlock && (y < 0 || y >= a.num_blocks)) {
+        y = kBadBlock;
+        any_bad = true;
+      }
+      s_ids[i] = int2{x, y};
+      s_rec[i] = rcd[k];
+    }
+  }
+  if (any_bad && a.dev_err)
+    atomicOr(a.dev_err, GKV_DEVERR_BLOCK_ID);
+  // The appends' stores complete, then the barrier: the waves of this
+  // workgroup share one CU and its caches, so every wave then reads the new
+  // tokens back.
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8)); // vmcnt(0)
+  __syncthreads();
+
+  // The stream reads its arguments afresh from the kernel-argument segment
+  // (the prologue's values are not kept live across the loop).
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef const __attribute__((address_space(4))) DecodeArgs *KernargPtr;
+  KernargPtr pa = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(pa));
+  const DecodeArgs a2 = *pa;
+  stream_range<R, VQ, true>(a2, w_id, s_ids, s_rec, s_len, n_steps);
+#endif
+}
+
 // ---- combine --------------------------------------------------------------------
 
 // One workgroup per sequence, wave g for kv head g; lane (h = lane / 8) merges
@@ -720,13 +965,13 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
 
 constexpr int kRing = 4;
 
-// Ring depth of the split kernel (default kRing; the tuning variable
-// GKV_DECODE_RING = 3..8 picks another, read once).
+// Ring depth of the split kernels (default kRing; the tuning variable
+// GKV_DECODE_RING = 3..5 picks another, read once).
 static int ring_depth() {
   static const int r = [] {
     const char *e = getenv("GKV_DECODE_RING");
     const int v = e ? atoi(e) : kRing;
-    return (v >= 3 && v <= 8) ? v : kRing;
+    return (v >= 3 && v <= 5) ? v : kRing;
   }();
   return r;
 }
@@ -739,20 +984,15 @@ static void launch_split_ring(const DecodeArgs &a, dim3 grid, dim3 block, hipStr
     hipLaunchKernelGGL((decode_split_kernel<R, false>), grid, block, 0, s, a);
 }
 
-static const void *split_kernel_fn(int ring) {
+// The fused kernel at the given ring depth (3..5; the default otherwise).
+static const void *fused_kernel_fn(int ring) {
   switch (ring) {
   case 3:
-    return (const void *)decode_split_kernel<3, false>;
+    return (const void *)decode_fused_kernel<3, false>;
   case 5:
-    return (const void *)decode_split_kernel<5, false>;
-  case 6:
-    return (const void *)decode_split_kernel<6, false>;
-  case 7:
-    return (const void *)decode_split_kernel<7, false>;
-  case 8:
-    return (const void *)decode_split_kernel<8, false>;
+    return (const void *)decode_fused_kernel<5, false>;
   default:
-    return (const void *)decode_split_kernel<4, false>;
+    return (const void *)decode_fused_kernel<4, false>;
   }
 }
 
@@ -769,7 +1009,7 @@ static int resident_workgroups(int n_kv_heads) {
   if (slot == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, split_kernel_fn(ring_depth()),
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fused_kernel_fn(ring_depth()),
                                                      split_block(n_kv_heads), 0) != hipSuccess)
       return 0;
     slot = std::max(1, cus * per_cu);
@@ -828,6 +1068,10 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
     return GKV_ERR_UNSUPPORTED;
   if (need_cache && q_stride < (int64_t)n_q_heads * kHeadDim)
     return GKV_ERR_ARG;
+  // 16-byte loads of the query rows and the angle tables
+  if (need_cache && (q_stride % 4 != 0 ||
+                     ((uintptr_t)q | (uintptr_t)cos_tab | (uintptr_t)sin_tab) % 16 != 0))
+    return GKV_ERR_ARG;
   if (out_stride < (int64_t)n_q_heads * kHeadDim)
     return GKV_ERR_ARG;
   if (split_tokens < 0 || split_tokens % kStep != 0)
@@ -836,6 +1080,8 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
     return GKV_ERR_ARG;
   if (cache.ring > 0 && window == 0)
     return GKV_ERR_ARG; // a ring holds only the last W tokens
+  if (need_cache && window > 0 && cache.ring == 0)
+    return GKV_ERR_UNSUPPORTED; // the window is read from a ring of W slots
   const int64_t t_max = stream_max(B, max_seq_len, window);
   if (t_max >= (1 << 30) || (int64_t)B << 8 >= INT32_MAX)
     return GKV_ERR_ARG;
@@ -931,19 +1177,41 @@ static int launch_split(const DecodeArgs &a, hipStream_t s) {
   case 5:
     launch_split_ring<5>(a, grid, block, s);
     break;
-  case 6:
-    launch_split_ring<6>(a, grid, block, s);
-    break;
-  case 7:
-    launch_split_ring<7>(a, grid, block, s);
-    break;
-  case 8:
-    launch_split_ring<8>(a, grid, block, s);
-    break;
   default:
     launch_split_ring<4>(a, grid, block, s);
   }
   return launch_status("decode_split_kernel");
+}
+
+template <int R>
+static void launch_fused_ring(const DecodeArgs &a, const AppendArgs &ap, int append, dim3 grid,
+                              dim3 block, hipStream_t s) {
+  if (a.vs)
+    hipLaunchKernelGGL((decode_fused_kernel<R, true>), grid, block, 0, s, a, ap, append);
+  else
+    hipLaunchKernelGGL((decode_fused_kernel<R, false>), grid, block, 0, s, a, ap, append);
+}
+
+// The fused launch; ap == nullptr: no append (attention only).
+static int launch_fused(const DecodeArgs &a, const AppendArgs *ap, hipStream_t s) {
+  const dim3 grid(a.n_wg), block(split_block(a.n_kv_heads));
+  AppendArgs aa{};
+  if (ap) {
+    aa = *ap;
+    aa.seq_lens = nullptr; // the kernel passes each row's position (its length - 1)
+  }
+  const int append = ap ? 1 : 0;
+  switch (ring_depth()) {
+  case 3:
+    launch_fused_ring<3>(a, aa, append, grid, block, s);
+    break;
+  case 5:
+    launch_fused_ring<5>(a, aa, append, grid, block, s);
+    break;
+  default:
+    launch_fused_ring<4>(a, aa, append, grid, block, s);
+  }
+  return launch_status("decode_fused_kernel");
 }
 
 static int launch_combine(const DecodeArgs &a, hipStream_t s) {
@@ -1017,9 +1285,7 @@ extern "C" int gkv_decode_attention(GKV_DECODE_PARAMS) {
   int st = GKV_DECODE_PREPARE(a);
   if (st != GKV_OK || B == 0)
     return st;
-  if ((st = launch_prep(a, stream_max(B, max_seq_len, window), (hipStream_t)stream)))
-    return st;
-  if ((st = launch_split(a, (hipStream_t)stream)))
+  if ((st = launch_fused(a, nullptr, (hipStream_t)stream)))
     return st;
   return launch_combine(a, (hipStream_t)stream);
 }
@@ -1080,11 +1346,14 @@ extern "C" int gkv_decode_layer_prepare(GKV_LAYER_PARAMS) {
   return launch_layer_prep(a, ap, stream_max(B, max_seq_len, window), (hipStream_t)stream);
 }
 
+extern "C" int gkv_decode_layer_split(GKV_LAYER_PARAMS) {
+  GKV_LAYER_SETUP
+  return launch_fused(a, &ap, (hipStream_t)stream);
+}
+
 extern "C" int gkv_decode_layer(GKV_LAYER_PARAMS) {
   GKV_LAYER_SETUP
-  if ((st = launch_layer_prep(a, ap, stream_max(B, max_seq_len, window), (hipStream_t)stream)))
-    return st;
-  if ((st = launch_split(a, (hipStream_t)stream)))
+  if ((st = launch_fused(a, &ap, (hipStream_t)stream)))
     return st;
   return launch_combine(a, (hipStream_t)stream);
 }

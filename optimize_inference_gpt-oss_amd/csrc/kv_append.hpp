@@ -67,15 +67,18 @@ struct RowPlace {
 
 // part / n_parts: the row may be shared by n_parts waves, wave `part` taking
 // every n_parts-th kv head (and query pair); a head's 4 key and 4 value lanes
-// stay adjacent in one wave (the int8 scale is their max). v_stage: NULL, or bf16 [Hkv * 64] in LDS that receives the
-// row's V; then the bf16 V cache store is left to the caller.
+// stay adjacent in one wave (the int8 scale is their max). v_stage: NULL, or
+// bf16 [Hkv * 64] in LDS that receives the row's V; then the bf16 V cache
+// store is left to the caller. pos_known >= 0: the row's position, already
+// known to the caller (no load of row_pos / seq_lens).
 __device__ __forceinline__ RowPlace append_row(const AppendArgs &a, int r, int lane,
                                                int part = 0, int n_parts = 1,
-                                               uint16_t *v_stage = nullptr) {
+                                               uint16_t *v_stage = nullptr,
+                                               int pos_known = -1) {
   constexpr int D = kHeadDim, HALF = kHeadDim / 2;
   const int seq = a.row_seq ? a.row_seq[r] : r;
   // the row's position: given, or the last position of its sequence
-  const int pos = a.row_pos ? a.row_pos[r] : a.seq_lens[seq] - 1;
+  const int pos = pos_known >= 0 ? pos_known : a.row_pos ? a.row_pos[r] : a.seq_lens[seq] - 1;
   const float *row = a.qkv + (int64_t)r * a.row_stride;
   const float *cs = a.cos_tab + (int64_t)pos * HALF, *sn = a.sin_tab + (int64_t)pos * HALF;
   const int kv_dim = a.n_kv_heads * D;

@@ -94,6 +94,9 @@ SIGNATURES = {
     "gkv_decode_layer": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
                                         CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
                                         _vp]),
+    "gkv_decode_layer_split": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
+                                        CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
+                                        _vp]),
     "gkv_decode_layer_prepare": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
                                         CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
                                         _vp]),
@@ -253,10 +256,11 @@ def decode_attention(q, seq_lens, max_seq_len, view: CacheView, sinks, out, wind
     out_dtype = BF16 if out.dtype == torch.bfloat16 else F32
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     args_common = (stream_handle(stream), q.shape[0])
-    if stage in ("both", "prepare", "split", "layer", "layer_prepare"):
+    if stage in ("both", "prepare", "split", "layer", "layer_prepare", "layer_split"):
         name = {"both": "gkv_decode_attention", "prepare": "gkv_decode_prepare",
                 "split": "gkv_decode_split", "layer": "gkv_decode_layer",
-                "layer_prepare": "gkv_decode_layer_prepare"}[stage]
+                "layer_prepare": "gkv_decode_layer_prepare",
+                "layer_split": "gkv_decode_layer_split"}[stage]
         st = getattr(lib(), name)(*args_common, sinks.shape[0], ptr(q), q.stride(0),
                                   ptr(cos_tab), ptr(sin_tab), ptr(seq_lens), max_seq_len, view,
                                   window, ptr(sinks), split_tokens, ptr(workspace), ws_bytes,
