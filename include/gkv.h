@@ -117,10 +117,11 @@ int gkv_rope_table(const gkv_rope_config *cfg, int32_t n_pos, float *cos_tab, fl
  * the paged cache at the row's slot. One row per token:
  *   row_pos[r]   position of row r's token (device int32)
  *   row_seq[r]   its sequence (device int32; NULL: row r is sequence r)
- *   seq_lens[s]  tokens of sequence s after this append (device int32; NULL:
- *                none). Only used on ring layers: a row whose slot a later
- *                row of this same call overwrites (pos + ring < seq_len) is
- *                not stored, so the ring ends up holding the last W positions.
+ *   seq_lens[s]  tokens of sequence s after this append (device int32;
+ *                required on ring layers, GKV_ERR_ARG if NULL there; unused
+ *                otherwise). A row whose ring slot a later row of this same
+ *                call overwrites (pos + ring < seq_len) is not stored, so the
+ *                ring ends up holding the last W positions.
  *   q_out        NULL, or fp32 [rows][q_out_stride] receiving the rotated Q
  *                (may equal qkv with q_out_stride = row_stride: in place)
  *   k_pack/v_pack NULL, or bf16 [rows][Hkv][64] receiving the same bf16 K, V

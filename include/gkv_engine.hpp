@@ -81,14 +81,17 @@ inline void gemm_bf16_rope_kv(stream_t s, const bf16_t *A, int M, const bf16_t *
 }
 
 // attention_bf16_chunk64 (getp-csrc/kernels/fast_attention.hpp:566-580): one
-// query row per sequence against its cache plus the head's sink, output bf16
-// [B][out_stride]. With q_rotated false the query is rotated on load at
+// query row per sequence against its cache (bf16 V; an int8-V layer is
+// GKV_ERR_ARG) plus the head's sink, output bf16 [B][out_stride]. With q_rotated false the query is rotated on load at
 // row_pos (the reference's cosv/sinv form, used after
 // rope_kv_bf16(rotate_q = false)).
 inline void attention_bf16_chunk64(stream_t s, const float *qkv, int row_stride,
                                    const PagedLayer &layer, int n_q_heads, bf16_t *out,
                                    int out_stride, int B, const PagedBatch &bt,
                                    bool q_rotated = false) {
+  if (layer.view.v_format != GKV_V_BF16)
+    check(GKV_ERR_ARG, "attention_bf16_chunk64 (the layer holds the int8-V cache: use "
+                       "attention_q8v_chunk64)");
   check(gkv_decode_attention(s, B, n_q_heads, qkv, row_stride, q_rotated ? nullptr : bt.cos_tab,
                              q_rotated ? nullptr : bt.sin_tab, bt.seq_lens, bt.max_seq_len,
                              layer.view, layer.window, layer.sinks, 0, bt.workspace,
@@ -96,9 +99,10 @@ inline void attention_bf16_chunk64(stream_t s, const float *qkv, int row_stride,
         "attention_bf16_chunk64");
 }
 
-// rope_kv_bf16(rotate_q = false) followed by attention_bf16_chunk64, the pair
-// at gpu_engine.hpp:495-498, as one gkv_decode_layer call (the append runs in
-// the attention's first launch). Row b is the new token at row_pos[b].
+// rope_kv_bf16(rotate_q = false) followed by attention_q8v_chunk64 (int8-V
+// layer) or attention_bf16_chunk64 (bf16 V), the pair at gpu_engine.hpp:495-498,
+// as one gkv_decode_layer call (the append runs in the attention's launch).
+// Row b is the new token at row_pos[b]; the output is bf16.
 inline void rope_kv_attention_bf16(stream_t s, int B, const float *qkv, int row_stride,
                                    const PagedLayer &layer, int n_q_heads, bf16_t *out,
                                    int out_stride, const PagedBatch &bt) {
@@ -109,16 +113,41 @@ inline void rope_kv_attention_bf16(stream_t s, int B, const float *qkv, int row_
         "rope_kv_attention_bf16");
 }
 
-// The exact path's fp32-output attention (attention_exact,
-// getp-csrc/kernels/attention.hpp:18-83), same arguments, fp32 [B][out_stride].
-inline void attention_exact(stream_t s, const float *qkv, int row_stride,
-                            const PagedLayer &layer, int n_q_heads, float *out, int out_stride,
-                            int B, const PagedBatch &bt, bool q_rotated = false) {
-  check(gkv_decode_attention(s, B, n_q_heads, qkv, row_stride, q_rotated ? nullptr : bt.cos_tab,
-                             q_rotated ? nullptr : bt.sin_tab, bt.seq_lens, bt.max_seq_len,
-                             layer.view, layer.window, layer.sinks, 0, bt.workspace,
-                             bt.workspace_bytes, out, out_stride, GKV_F32, bt.dev_err),
-        "attention_exact");
+// attention_q8v_chunk64 (getp-csrc/kernels/fast_attention.hpp:604-622), the
+// call of the engine's fast path (layer_attention, gpu_engine.hpp:497-498),
+// in the reference's argument order: the cache arguments (kc, vq, vs, slots)
+// become the layer's paged view, which must hold the int8-V cache
+// (GKV_V_INT8; else GKV_ERR_ARG), and the scalar pos becomes the batch's
+// per-row positions. kv_dim = Hkv * 64 and, as in the reference's
+// attention_gqa8 kernels, 8 query heads per kv head. window is the layer's
+// (0 or its ring). rotate_q stands for the reference's cosv/sinv: true = the
+// query is rotated on load at each row's position (cos/sin from bt).
+inline void attention_q8v_chunk64(stream_t s, const float *qkv, int row_stride,
+                                  const PagedLayer &layer, int kv_dim, const float *sinks,
+                                  bf16_t *out, int out_stride, int B, const PagedBatch &bt,
+                                  int window, bool rotate_q = true) {
+  if (layer.view.v_format != GKV_V_INT8 || kv_dim != layer.view.n_kv_heads * 64 ||
+      window != layer.view.ring)
+    check(GKV_ERR_ARG, "attention_q8v_chunk64");
+  const int n_q_heads = 8 * (kv_dim / 64);
+  check(gkv_decode_attention(s, B, n_q_heads, qkv, row_stride, rotate_q ? bt.cos_tab : nullptr,
+                             rotate_q ? bt.sin_tab : nullptr, bt.seq_lens, bt.max_seq_len,
+                             layer.view, window, sinks, 0, bt.workspace, bt.workspace_bytes, out,
+                             out_stride, GKV_BF16, bt.dev_err),
+        "attention_q8v_chunk64");
+}
+
+// The reference's exact path (attention_exact, getp-csrc/kernels/attention.hpp:18-83,
+// bit-for-bit with the CPU forward) attends over fp32 caches with fp64 score
+// sums. The paged pool stores bf16 K and bf16 or int8 V, so no call here can
+// reproduce those bits: this entry point reports GKV_ERR_UNSUPPORTED (print
+// and exit, like every shim failure) instead of silently running the
+// tolerance path under the exact path's name.
+inline void attention_exact(stream_t, const float *, int, const PagedLayer &, int, float *, int,
+                            int, const PagedBatch &, bool = false) {
+  check(GKV_ERR_UNSUPPORTED, "attention_exact (fp32 caches are not built; use "
+                             "attention_bf16_chunk64 or attention_q8v_chunk64, tolerance "
+                             "2e-3 abs + 1e-2 rel)");
 }
 
 } // namespace gkv_engine

@@ -19,7 +19,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libgkv.so")
-DEMO = os.path.join(HERE, "gkv_engine_demo")
+DEMO = os.path.join(ROOT, "tests", "gkv_engine_demo")  # test driver of the C++ shim
 
 SOURCES = [
     "kv_append.hip",
@@ -62,10 +62,11 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
-    # the C++ engine-shim demo: host code only, linked against libgkv.so
+    # the C++ engine-shim test driver (tests/engine_demo.cpp): host code only,
+    # linked against libgkv.so
     cmd = [HIPCC, "-std=c++17", "-O2", "-x", "c++", "-D__HIP_PLATFORM_AMD__", "-I", "/opt/rocm/include", "-I",
-           os.path.join(ROOT, "include"), os.path.join(CSRC, "engine_demo.cpp"), "-o",
-           DEMO + ".tmp", "-L", HERE, "-lgkv", "-Wl,-rpath,$ORIGIN"]
+           os.path.join(ROOT, "include"), os.path.join(ROOT, "tests", "engine_demo.cpp"), "-o",
+           DEMO + ".tmp", "-L", HERE, "-lgkv", "-Wl,-rpath,$ORIGIN/../optimize_inference_gpt-oss_amd"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"engine demo build failed:\n{r.stderr}")

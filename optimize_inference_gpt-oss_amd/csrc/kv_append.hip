@@ -113,6 +113,10 @@ extern "C" int gkv_kv_append(void *stream, int32_t n_rows, const float *qkv, int
     return GKV_ERR_ARG;
   if (to_cache && cache.v_format == GKV_V_INT8 && !cache.v_scale)
     return GKV_ERR_ARG;
+  // On a ring, two rows of one sequence W positions apart take the same slot;
+  // only the lengths tell which of them the ring keeps.
+  if (to_cache && cache.ring > 0 && !seq_lens)
+    return GKV_ERR_ARG;
   if (n_rows == 0)
     return GKV_OK;
   AppendArgs a;

@@ -191,10 +191,8 @@ __global__ __launch_bounds__(64 * kNW) void qkv_append_kernel(QkvArgs a) {
       acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   place_hop1();
-  dma(0, 0);
-  dma(1, 1);
 #pragma unroll
-  for (int p = 2; p < kGStages - 1; p++)
+  for (int p = 0; p < kGStages - 1; p++)
     dma(p, p);
   int st = 0;
   for (int kc = 0; kc < nk; kc++) {
@@ -354,6 +352,8 @@ extern "C" int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64
     return GKV_ERR_ARG;
   if (to_cache && !row_pos && !seq_lens)
     return GKV_ERR_ARG; // no way to find the rows' positions
+  if (to_cache && cache.ring > 0 && !seq_lens)
+    return GKV_ERR_ARG; // rows W positions apart share a ring slot: the lengths pick the kept one
   if (cache.ring % kBlockTokens != 0)
     return GKV_ERR_UNSUPPORTED;
   if (cache.v_format != GKV_V_BF16 && cache.v_format != GKV_V_INT8)

@@ -5,8 +5,10 @@
 // tables, then per layer rope_kv_bf16(rotate_q = false) and
 // attention_bf16_chunk64 with the query rotated on load.
 //
-//   gkv_engine_demo <in.bin> <out.bin> [fused | project]
+//   gkv_engine_demo <in.bin> <out.bin> [fused | project | q8v]
 // fused: the one-call form rope_kv_attention_bf16 instead of the two calls.
+// q8v: the engine's own fast-path pair, rope_kv_bf16 + attention_q8v_chunk64
+//   (gpu_engine.hpp:495-498; the pool must hold the int8-V cache).
 // project: the qkv rows come from the layer input through the QKV projection
 //   with the append in its epilogue (gemm_bf16_rope_kv, the pair
 //   gemm_bf16 + rope_kv_bf16 of gpu_engine.hpp:493-496), then
@@ -39,11 +41,12 @@
 
 int main(int argc, char **argv) {
   if (argc != 3 && argc != 4) {
-    fprintf(stderr, "usage: %s in.bin out.bin [fused | project]\n", argv[0]);
+    fprintf(stderr, "usage: %s in.bin out.bin [fused | project | q8v]\n", argv[0]);
     return 2;
   }
   const bool fused = argc == 4 && std::string(argv[3]) == "fused";
   const bool project = argc == 4 && std::string(argv[3]) == "project";
+  const bool q8v = argc == 4 && std::string(argv[3]) == "q8v";
   FILE *f = fopen(argv[1], "rb");
   if (!f)
     return 2;
@@ -155,6 +158,11 @@ int main(int argc, char **argv) {
                               (size_t)B * QKV * 4, hipMemcpyHostToDevice, s));
         if (fused) {
           gkv_engine::rope_kv_attention_bf16(s, B, d_qkv, QKV, layers[l], Hq, d_out, ATT, bt);
+        } else if (q8v) {
+          // layer_attention's lines, the cache arguments replaced by the paged layer
+          gkv_engine::rope_kv_bf16(s, B, d_qkv, QKV, bt, Hq, layers[l], /*rotate_q=*/false);
+          gkv_engine::attention_q8v_chunk64(s, d_qkv, QKV, layers[l], Hkv * 64, layers[l].sinks,
+                                            d_out, ATT, B, bt, layers[l].window);
         } else {
           gkv_engine::rope_kv_bf16(s, B, d_qkv, QKV, bt, Hq, layers[l], /*rotate_q=*/false);
           gkv_engine::attention_bf16_chunk64(s, d_qkv, QKV, layers[l], Hq, d_out, ATT, B, bt);

@@ -81,6 +81,9 @@ def test_append_argument_checks(gkv):
     assert call(args(hq=60)) == gkv.GKV_ERR_ARG                # not a multiple of Hkv
     assert call(args(view=_view(gkv, ring=100))) == gkv.GKV_ERR_UNSUPPORTED
     assert call(args(view=_view(gkv, num_blocks=0))) == gkv.GKV_ERR_ARG
+    # a ring needs the lengths: rows W positions apart share a slot
+    assert call(args(view=_view(gkv, ring=128))) == gkv.GKV_ERR_ARG
+    assert call(args(n=0, view=_view(gkv, ring=128), lens=fake)) == gkv.GKV_OK
     assert call(args(n=0)) == gkv.GKV_OK                        # nothing to do
 
 
@@ -107,6 +110,7 @@ def test_qkv_append_argument_checks(gkv):
     assert call(args(cos=None)) == gkv.GKV_ERR_ARG              # the append needs the angles
     assert call(args(lens=None)) == gkv.GKV_ERR_ARG             # no way to find positions
     assert call(args(view=_view(gkv, ring=100))) == gkv.GKV_ERR_UNSUPPORTED
+    assert call(args(view=_view(gkv, ring=128), pos=fake, lens=None)) == gkv.GKV_ERR_ARG
     assert call(args(view=_view(gkv, k=None, v=None), out=None)) == gkv.GKV_ERR_ARG  # no output
     assert call(args(n=0)) == gkv.GKV_OK                         # nothing to do
     # projection only: no cache, no angles needed
@@ -130,6 +134,8 @@ def test_decode_argument_checks(gkv):
     assert call(dtype=7) == gkv.GKV_ERR_ARG
     assert call(view=_view(gkv, ring=128), window=0) == gkv.GKV_ERR_ARG
     assert call(view=_view(gkv, ring=64), window=128) == gkv.GKV_ERR_ARG
+    # a window is read from a ring of W slots, not from a full-length cache
+    assert call(view=_view(gkv, ring=0), window=128) == gkv.GKV_ERR_UNSUPPORTED
     # a workspace of the advertised size is required
     need = gkv.workspace_bytes(4, 8, 5000)
     assert need > 0

@@ -1,6 +1,7 @@
 """The C++ engine shim (include/gkv_engine.hpp) driven the way the reference
-engine drives its attention: a C++ decode loop (csrc/engine_demo.cpp, built by
-build()) calls rope_kv_bf16 + attention_bf16_chunk64 per layer and step over
+engine drives its attention: a C++ decode loop (tests/engine_demo.cpp, built by
+build()) calls rope_kv_bf16 + attention_bf16_chunk64 (or, on the int8-V cache,
+the engine's own pair rope_kv_bf16 + attention_q8v_chunk64) per layer and step over
 the paged pool (one window layer with a wrapping 32-slot ring, one full
 layer). Every step's bf16 output is compared with the CPU oracle, which keeps
 the history by position: max-abs 2e-3 + rel 1e-2, plus bf16 output rounding.
@@ -17,7 +18,7 @@ from kvcase import allclose_report
 pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-DEMO = os.path.join(ROOT, "optimize_inference_gpt-oss_amd", "gkv_engine_demo")
+DEMO = os.path.join(ROOT, "tests", "gkv_engine_demo")
 
 
 def _bf16_values(a):
@@ -27,9 +28,10 @@ def _bf16_values(a):
 
 
 @pytest.mark.parametrize("mode,v_int8", [(None, False), ("fused", False), ("fused", True),
-                                         ("project", False)])
+                                         ("project", False), ("q8v", True)])
 def test_engine_shim_decode_loop(oracle, cuda, tmp_path, mode, v_int8):
-    """mode None: rope_kv_bf16 + attention_bf16_chunk64; "fused": the one-call
+    """mode None: rope_kv_bf16 + attention_bf16_chunk64; "q8v": rope_kv_bf16 +
+    attention_q8v_chunk64 in the reference's argument order; "fused": the one-call
     rope_kv_attention_bf16; "project": the qkv rows come from the layer input
     through gemm_bf16_rope_kv (projection with the append in its epilogue),
     and the oracle's rows from orc_linear (run.cpp matmul + bias)."""
@@ -82,3 +84,22 @@ def test_engine_shim_decode_loop(oracle, cuda, tmp_path, mode, v_int8):
                                           window=window)
             n_bad, max_err = allclose_report(got[p, l], ref, 2e-3, 1e-2 + 2 ** -8)
             assert n_bad == 0, f"layer {l} step {p}: {n_bad} bad, max err {max_err}"
+
+
+@pytest.mark.parametrize("mode,v_int8", [(None, True), ("q8v", False)])
+def test_engine_shim_rejects_mismatched_cache(cuda, tmp_path, mode, v_int8):
+    """attention_bf16_chunk64 on an int8-V pool, and attention_q8v_chunk64 on a
+    bf16 one, fail loudly (the shim prints and exits, as the reference's
+    HIP_CHECK does) instead of reading the cache in the wrong format."""
+    if not os.path.exists(DEMO):
+        pytest.fail("gkv_engine_demo is not built (run __graft_entry__.build())")
+    P, B, Hq, Hkv, NL, W = 2, 1, 64, 8, 2, 32
+    inp, outp = tmp_path / "in.bin", tmp_path / "out.bin"
+    with open(inp, "wb") as f:
+        np.array([P, B, Hq, Hkv, NL, W, 1 if v_int8 else 0], np.int32).tofile(f)
+        np.zeros((P, NL, B, (Hq + 2 * Hkv) * 64), np.float32).tofile(f)
+        np.zeros((NL, Hq), np.float32).tofile(f)
+    cmd = [DEMO, str(inp), str(outp)] + ([mode] if mode else [])
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=90)
+    assert r.returncode != 0
+    assert "attention_" in r.stderr and "bad argument" in r.stderr, r.stderr

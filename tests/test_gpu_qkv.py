@@ -105,10 +105,12 @@ def run(case, gkv, torch, dev, cache=True):
     return res
 
 
-def check_projection(case, res, oracle):
-    ref = oracle.linear(case.x, case.w, case.bias)
-    scale = np.abs(case.x).astype(np.float64) @ np.abs(case.w).astype(np.float64).T
-    err = np.abs(res["qkv"].astype(np.float64) - ref)
+def check_projection(case, res, oracle, rows=None):
+    """rows: the rows checked (default: all)."""
+    rows = np.arange(case.M) if rows is None else np.asarray(rows)
+    ref = oracle.linear(case.x[rows], case.w, case.bias)
+    scale = np.abs(case.x[rows]).astype(np.float64) @ np.abs(case.w).astype(np.float64).T
+    err = np.abs(res["qkv"][rows].astype(np.float64) - ref)
     bad = err > 2e-5 * scale + 1e-6
     assert not bad.any(), f"{int(bad.sum())} projections out of bound, max err {err.max()}"
 
@@ -213,6 +215,25 @@ def test_many_rows_large_tiles(oracle, gkv, cuda):
     res = run(case, gkv, torch, cuda)
     assert res["err"] == 0
     check_projection(case, res, oracle)
+    check_cache(case, res, oracle)
+
+
+@pytest.mark.parametrize("v_int8", [False, True])
+def test_gpt_oss_shape_large_tiles(oracle, gkv, cuda, v_int8):
+    """A prompt batch of the gpt-oss shape (Hq 64, Hkv 8, hidden 2880, N 5120)
+    past 2,048 rows: the 128 x 128 tiles with their 40 column blocks spread
+    over the XCDs, a ragged last row block, bf16 and int8 V. Every cache byte
+    is checked; the projection on 300 sampled rows and every row of the last
+    row block."""
+    import torch
+    case = QkvCase(17 + int(v_int8), 64, 8, 2880, prompts=[800, 640, 512, 130], v_int8=v_int8)
+    assert case.M >= 2048 and case.M % 128 != 0
+    res = run(case, gkv, torch, cuda)
+    assert res["err"] == 0
+    rng = np.random.default_rng(3)
+    rows = np.unique(np.concatenate([rng.choice(case.M, 300, replace=False),
+                                     np.arange(case.M // 128 * 128, case.M)]))
+    check_projection(case, res, oracle, rows)
     check_cache(case, res, oracle)
 
 
