@@ -40,6 +40,61 @@ HBM_PEAK_GBS = 8000.0
 D = 64
 
 
+def source_hash() -> str:
+    """sha256 over the library's sources (kernels, host code, the C ABI
+    header): a profile summary records it, and bench uses that summary's
+    traffic figure only for a build of the same sources."""
+    import hashlib
+    h = hashlib.sha256()
+    files = [os.path.join(PKG, "csrc", f) for f in sorted(os.listdir(os.path.join(PKG, "csrc")))]
+    files.append(os.path.join(ROOT, "include", "gkv.h"))
+    for path in files:
+        h.update(os.path.basename(path).encode())
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def load_traffic(name: str):
+    """(HBM bytes per launch, note) from profiles/<name>.json: measured
+    (rocprofv3 FETCH_SIZE and WRITE_SIZE, scaled by a plain copy) for the
+    dominant kernel of this run. None when the summary is missing or was
+    measured on other sources than the ones this build comes from."""
+    path = os.path.join(ROOT, "profiles", name + ".json")
+    if not os.path.exists(path):
+        return None, f"no profiles/{name}.json"
+    with open(path) as f:
+        rec = json.load(f)
+    if rec.get("source_sha256") != source_hash():
+        return None, f"profiles/{name}.json was measured on other sources (stale): not used"
+    return rec.get("hbm_bytes_per_launch"), f"profiles/{name}.json (sources {source_hash()[:12]})"
+
+
+def host_cpu():
+    """(model name, physical cores) of this machine, from /proc/cpuinfo."""
+    model, cores = "unknown", set()
+    try:
+        phys = core = None
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name":
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+        if phys is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    return model, len(cores) or (os.cpu_count() or 1)
+
+
 def load_gkv():
     spec = importlib.util.spec_from_file_location("gkv", os.path.join(PKG, "gkv.py"))
     mod = importlib.util.module_from_spec(spec)
@@ -307,11 +362,7 @@ def run_prefill(torch, gkv, args) -> int:
     # (2500 TFLOP/s / 8 TB/s = 312 FLOP/B): HBM is the bound of this kernel.
     alg_bytes = float(T * Hq * D * 4 + T * Hkv * D * 2 * 2 + T * Hq * D * 2)
     achieved = alg_bytes / (dom_ms * 1e-3) / 1e9
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "prefill_config4_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic, traffic_note = load_traffic("prefill_config4_traffic")
     line = {
         "metric": "causal prefill attention throughput (TFLOP/s), config 4",
         "value": round(sum(fl) / (ms_per_step * 1e-3) / 1e12, 2),
@@ -333,7 +384,8 @@ def run_prefill(torch, gkv, args) -> int:
         },
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "kernel": "prefill_kernel",
+                     "traffic": traffic, "traffic_source": traffic_note,
+                     "kernel": "prefill_kernel",
                      "kernel_us": round(dom_ms * 1e3, 2), "algorithmic_bytes": alg_bytes,
                      "mfma": {"achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                               "unit": "TFLOP/s",
@@ -407,11 +459,9 @@ def run_qkv(torch, gkv, args) -> int:
     flops = 2.0 * B * N * hidden
     tflops = flops / (ms * 1e-3) / 1e12
     alg_bytes = float(B * hidden * 2 + N * hidden * 2 + N * 4 + B * N * 4 + B * Hkv * D * 2 * 2)
-    traffic = None  # measured for config 2's 512 rows only
-    tpath = os.path.join(ROOT, "profiles", "qkv_append_config2_traffic.json")
-    if B == cfg["B"] and os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic, traffic_note = None, "measured for config 2's 512 rows only"
+    if B == cfg["B"]:
+        traffic, traffic_note = load_traffic("qkv_append_config2_traffic")
     line = {
         "metric": "QKV projection + KV append throughput (TFLOP/s)",
         "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -426,6 +476,7 @@ def run_qkv(torch, gkv, args) -> int:
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_note,
                      "kernel": "qkv_append_kernel", "kernel_us": round(ms * 1e3, 2),
                      "algorithmic_flops": flops,
                      "hbm": {"algorithmic_bytes": alg_bytes,
@@ -610,19 +661,25 @@ def main() -> int:
     dom_bytes = float(np.mean([bytes_of(layers[i]) for i in full]))
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
 
-    traffic = None
     vsfx = "_int8" if args.v_int8 else ""
-    tpath = os.path.join(ROOT, "profiles", f"decode_split_config{args.config}{vsfx}_traffic.json")
-    if os.path.exists(tpath) and not args.split_tokens:
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    kname = "decode_fused" if stages[0] == "append+split" else "decode_split"
+    traffic, traffic_note = None, "measured for the balanced split only"
+    if not args.split_tokens:
+        traffic, traffic_note = load_traffic(f"{kname}_config{args.config}{vsfx}_traffic")
 
     cpu = None
     if args.cpu_sample != 0:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        # OpenMP threads: --cpu-threads, else OMP_NUM_THREADS (the GPU box sets it to
+        # its CPU share for one GPU, 16), else every physical core of the host
+        model, phys = host_cpu()
+        threads = args.cpu_threads or int(os.environ.get("OMP_NUM_THREADS") or 0) or phys
         n_cpu = B if args.cpu_sample < 0 else min(args.cpu_sample, B)
         cpu = cpu_baseline(torch, gkv, pool, layers[full[0]], L, cfg, layers[full[0]].out,
                            n_cpu, threads, args.cpu_seconds, layer_index=full[0])
+        cpu["cpu_model"] = model
+        cpu["host_physical_cores"] = phys
+        cpu["threads_from"] = ("--cpu-threads" if args.cpu_threads else "OMP_NUM_THREADS"
+                               if os.environ.get("OMP_NUM_THREADS") else "physical cores")
 
     value = kv_bytes / (ms_per_step * 1e-3) / 1e9
     line = {
@@ -654,8 +711,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "decode_fused_kernel" if stages[0] == "append+split" else
-                      "decode_split_kernel",
+            "traffic_source": traffic_note,
+            "kernel": kname + "_kernel",
             "kernel_us": round(dom_ms * 1e3, 2),
             "algorithmic_bytes": dom_bytes,
         },
