@@ -73,7 +73,8 @@ constexpr int kStep = 32;              // tokens per wave step
 constexpr int kCols = 8;               // query heads per kv head handled (G <= 8)
 constexpr int kMlStride = 16;          // floats of (m, l) per partial: 8 heads x 2
 constexpr int kPartFloats = kCols * kHeadDim;
-constexpr int kMaxWorkgroups = 2048;   // split workgroups per launch (workspace bound)
+constexpr int kMaxWorkgroups = 1024;   // split workgroups per launch (workspace bound)
+constexpr int kPartsPerRange = 2;      // partial results per range: its first and its last segment
 constexpr int kPlanHeader = 4;         // ints: T, S, workgroups used, unused
 constexpr int kMaxRange = 16384;       // tokens per range (its ids and records sit in LDS)
 constexpr int kIdSlab = kMaxRange / kBlockTokens; // block ids per range (its slab in the workspace)
@@ -111,8 +112,8 @@ struct DecodeArgs {
                       // [range][kIdSlab], block k of range w at w * kIdSlab + k
   int32_t *steps;     // step record of every 32-token step: [range][kInfoSlab]
   u32x4 *qops;        // [B][Hkv][64 lanes][2]: query operands
-  float *ws_o;        // [B + kMaxWorkgroups][Hkv][8][64]
-  float *ws_ml;       // [B + kMaxWorkgroups][Hkv][8][2]
+  float *ws_o;        // [range][kPartsPerRange][Hkv][8][64]: partial outputs
+  float *ws_ml;       // [range][kPartsPerRange][Hkv][8][2]: their (m, l)
   void *out;
   int64_t out_stride;
   int out_bf16;
@@ -493,6 +494,7 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
   int cur_b = 0, cur_g = 0;   // its sequence and kv head
   float cur_sink = 0.0f;      // its sink (log2 units)
   bool cur_whole = false;     // the segment began at its sequence's first step
+  bool cur_first = false;     // the segment began at the range's first step
   bool cur_ends = false;      // ... and has reached its last step
   float m_run = 0.0f;         // running reference max (log2 units) of this column
   float lsum = 0.0f;
@@ -535,7 +537,10 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
         }
       }
     } else {
-      const int64_t part = ((int64_t)(cur_b + w_id)) * a.n_kv_heads + cur_g;
+      // only a range's first and last segments can be pieces of a longer
+      // sequence: partial slot 0 for the first, 1 for the last
+      const int64_t part =
+          ((int64_t)w_id * kPartsPerRange + (cur_first ? 0 : 1)) * a.n_kv_heads + cur_g;
       float *wo = a.ws_o + part * kPartFloats + head * D + 4 * kg;
 #pragma unroll
       for (int nn = 0; nn < 4; nn++)
@@ -548,7 +553,8 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
   };
 
   auto compute_step = [&](u32x4 (&kr)[4], u32x4 (&vr)[4], u32x4 (&qr)[QN], int rc, int bb,
-                          bool in_range) {
+                          int v) {
+    const bool in_range = v <= last_v;
     const int pass = bb >> 2;
     const int key = (rc >> 8) | (pass << 16);
     if (in_range && key != cur_key) {
@@ -560,6 +566,7 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
       cur_g = wv + pass * n_waves;
       cur_sink = pass ? sink_p[1] : sink_p[0];
       cur_whole = (rc & 0x80) != 0;
+      cur_first = v == pass * n_steps;
       m_run = cur_sink;
       lsum = 0.0f;
 #pragma unroll
@@ -700,7 +707,7 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
       const int slot = (r + R - 1) % R;
       load_step(min(v + R - 1, last_v), kbuf[slot], vbuf[slot], qbuf[slot], rec[slot],
                 badb[slot]);
-      compute_step(kbuf[r], vbuf[r], qbuf[r], rec[r], badb[r], v <= last_v);
+      compute_step(kbuf[r], vbuf[r], qbuf[r], rec[r], badb[r], v);
     }
   }
   flush();
@@ -941,13 +948,20 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
   if (w0 == w1)
     return; // finished by its split workgroup
   const float sk = a.sinks[g * a.G + h] * kLog2e;
+  // the sequence's piece in range w: that range's last segment (slot 1) for
+  // the first range unless the sequence starts exactly there, else its
+  // first segment (slot 0)
+  auto part_of = [&](int w) -> int64_t {
+    const int slot = (w == w0 && c0 != w0 * S) ? 1 : 0;
+    return ((int64_t)w * kPartsPerRange + slot) * a.n_kv_heads + g;
+  };
   float M = sk;
   for (int w = w0; w <= w1; w++)
-    M = fmaxf(M, a.ws_ml[((int64_t)(b + w) * a.n_kv_heads + g) * kMlStride + 2 * h]);
+    M = fmaxf(M, a.ws_ml[part_of(w) * kMlStride + 2 * h]);
   float Ls = __builtin_amdgcn_exp2f(sk - M);
   f32x4 o0 = {0, 0, 0, 0}, o1 = {0, 0, 0, 0};
   for (int w = w0; w <= w1; w++) {
-    const int64_t part = (int64_t)(b + w) * a.n_kv_heads + g;
+    const int64_t part = part_of(w);
     const float c = __builtin_amdgcn_exp2f(a.ws_ml[part * kMlStride + 2 * h] - M);
     Ls = fmaf(a.ws_ml[part * kMlStride + 2 * h + 1], c, Ls);
     const f32x4 *po = (const f32x4 *)(a.ws_o + part * kPartFloats + h * D + d0);
@@ -1019,22 +1033,24 @@ static int resident_workgroups(int n_kv_heads) {
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Workspace layout: plan | block ids | step records | query operands |
-// partials (o) | partials (m, l).
+// Workspace layout: plan | partials (o) | partials (m, l) | then, for the
+// staged launches only: block ids | step records | query operands. The split
+// that plans in its prologue uses the first three (fused_total bytes).
 struct WorkspaceLayout {
-  size_t plan, flat, steps, qops, ws_o, ws_ml, total;
+  size_t plan, ws_o, ws_ml, flat, steps, qops, fused_total, total;
 };
 
-static WorkspaceLayout layout_of(int B, int n_kv_heads, int64_t t_max) {
+static WorkspaceLayout layout_of(int B, int n_kv_heads, int max_wg) {
   WorkspaceLayout L;
   L.plan = 0;
-  L.flat = align256((size_t)(kPlanHeader + B + 1) * 4);
-  L.steps = L.flat + align256((size_t)kMaxWorkgroups * kIdSlab * 4);
-  L.qops = L.steps + align256((size_t)kMaxWorkgroups * kInfoSlab * 4);
-  L.ws_o = L.qops + align256((size_t)B * n_kv_heads * 64 * 32);
-  const size_t parts = (size_t)(B + kMaxWorkgroups) * n_kv_heads;
+  L.ws_o = align256((size_t)(kPlanHeader + B + 1) * 4);
+  const size_t parts = (size_t)kPartsPerRange * max_wg * n_kv_heads;
   L.ws_ml = L.ws_o + parts * kPartFloats * sizeof(float);
-  L.total = L.ws_ml + parts * kMlStride * sizeof(float);
+  L.flat = align256(L.ws_ml + parts * kMlStride * sizeof(float));
+  L.fused_total = L.flat;
+  L.steps = L.flat + align256((size_t)max_wg * kIdSlab * 4);
+  L.qops = L.steps + align256((size_t)max_wg * kInfoSlab * 4);
+  L.total = L.qops + align256((size_t)B * n_kv_heads * 64 * 32);
   return L;
 }
 
@@ -1095,7 +1111,7 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
     if (n_wg > kMaxWorkgroups)
       return GKV_ERR_ARG;
   }
-  const WorkspaceLayout L = layout_of(B, cache.n_kv_heads, t_max);
+  const WorkspaceLayout L = layout_of(B, cache.n_kv_heads, kMaxWorkgroups);
   if (!workspace || workspace_bytes_given < L.total)
     return GKV_ERR_WORKSPACE;
   if (split_tokens == 0) {
@@ -1228,7 +1244,7 @@ extern "C" size_t gkv_decode_workspace_bytes(int32_t B, int32_t n_kv_heads, int3
   (void)split_tokens;
   if (B < 0 || n_kv_heads <= 0 || max_seq_len < 0 || window < 0)
     return 0;
-  return layout_of(B, n_kv_heads, stream_max(B, max_seq_len, window)).total;
+  return layout_of(B, n_kv_heads, kMaxWorkgroups).total;
 }
 
 #define GKV_DECODE_PARAMS                                                                   \

@@ -147,17 +147,19 @@ def test_decode_argument_checks(gkv):
 
 
 def test_workspace_formula(gkv):
-    # plan (header + prefix sums), block ids (1024 per range) and step records
-    # (512 per range: ranges of up to 16384 tokens) for up to 2048 ranges, query operands (2 KB per sequence
-    # and kv head), each 256-byte aligned, then (B + 2048) partials of 8 heads
-    # x (64 + 2) floats per kv head
+    # plan (header + prefix sums); partial results of 2 segments per range for
+    # up to 1024 ranges, 8 heads x (64 + 2) floats per kv head; then, for the
+    # staged launches, block ids (1024 per range) and step records (512 per
+    # range: ranges of up to 16384 tokens) and the query operands (2 KB per
+    # sequence and kv head); each part 256-byte aligned
     def a256(x):
         return (x + 255) // 256 * 256
 
     B, hkv = 512, 8
-    fixed = a256((4 + B + 1) * 4) + a256(2048 * 1024 * 4) + a256(2048 * 512 * 4)
-    fixed += a256(B * hkv * 2048)
-    assert gkv.workspace_bytes(B, hkv, 2049) == fixed + (B + 2048) * hkv * (512 + 16) * 4
+    parts = 2 * 1024 * hkv
+    fused = a256(a256((4 + B + 1) * 4) + parts * (512 + 16) * 4)
+    staged = a256(1024 * 1024 * 4) + a256(1024 * 512 * 4) + a256(B * hkv * 2048)
+    assert gkv.workspace_bytes(B, hkv, 2049) == fused + staged
     # a window layer bounds the stream by the window
     assert gkv.workspace_bytes(B, hkv, 100000, window=128) == gkv.workspace_bytes(B, hkv, 128)
 
