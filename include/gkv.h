@@ -236,6 +236,21 @@ int gkv_decode_layer_prepare(void *stream, int32_t B, int32_t n_q_heads, const f
                              void *workspace, size_t workspace_bytes, void *out,
                              int64_t out_stride, int32_t out_dtype, uint32_t *dev_err);
 
+/* gkv_decode_layer without a workspace argument and without allocating: the
+ * workspace is the library's own device array (one per GPU, about 16.5 MiB,
+ * held until the process ends), looked up once per device. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments and results as gkv_decode_layer with
+ * split_tokens = 0. Limits: at most 8 kv heads, 8192 sequences and 512 split
+ * ranges (ranges hold up to 16384 tokens; more: GKV_ERR_CAPACITY). Calls that
+ * overlap on one GPU share the array and race: keep them on one stream. */
+int gkv_decode_layer_noalloc(void *stream, int32_t B, int32_t n_q_heads, const float *qkv,
+                             int64_t row_stride, const float *cos_tab, const float *sin_tab,
+                             const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,
+                             int32_t window, const float *sinks, void *out, int64_t out_stride,
+                             int32_t out_dtype, uint32_t *dev_err);
+
 /* ---- Prefill (causal) attention ----------------------------------------- */
 
 /* Causal attention of packed prompts with sinks: row j of prompt b (rows

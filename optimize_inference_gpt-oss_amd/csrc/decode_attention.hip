@@ -61,6 +61,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 
 namespace gkv {
 
@@ -1064,7 +1065,8 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
                    int32_t max_seq_len, const gkv_cache_view &cache, int32_t window,
                    const float *sinks, int32_t split_tokens, void *workspace,
                    size_t workspace_bytes_given, void *out, int64_t out_stride,
-                   int32_t out_dtype, uint32_t *dev_err, bool need_cache) {
+                   int32_t out_dtype, uint32_t *dev_err, bool need_cache,
+                   int ws_wg = kMaxWorkgroups, bool staged_parts = true) {
   if (B < 0 || n_q_heads <= 0 || cache.n_kv_heads <= 0 || !seq_lens || !sinks || !out ||
       max_seq_len < 0 || window < 0 || (out_dtype != GKV_F32 && out_dtype != GKV_BF16))
     return GKV_ERR_ARG;
@@ -1111,8 +1113,8 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
     if (n_wg > kMaxWorkgroups)
       return GKV_ERR_ARG;
   }
-  const WorkspaceLayout L = layout_of(B, cache.n_kv_heads, kMaxWorkgroups);
-  if (!workspace || workspace_bytes_given < L.total)
+  const WorkspaceLayout L = layout_of(B, cache.n_kv_heads, ws_wg);
+  if (!workspace || workspace_bytes_given < (staged_parts ? L.total : L.fused_total))
     return GKV_ERR_WORKSPACE;
   if (split_tokens == 0) {
     const int resident = (need_cache && B > 0) ? resident_workgroups(cache.n_kv_heads) : 1;
@@ -1122,6 +1124,8 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
     if (n_wg > kMaxWorkgroups)
       return GKV_ERR_ARG;
   }
+  if (n_wg > ws_wg)
+    return GKV_ERR_CAPACITY; // more ranges than the workspace has partial slots for
   a.q = q;
   a.q_stride = q_stride;
   a.cos_tab = cos_tab;
@@ -1374,3 +1378,72 @@ extern "C" int gkv_decode_layer(GKV_LAYER_PARAMS) {
   return launch_combine(a, (hipStream_t)stream);
 }
 
+
+// ---- decode layer without allocation ---------------------------------------------
+//
+// gkv_decode_layer with its workspace in this library's own device memory: a
+// file-scope array, one per GPU, held until the process ends. Its address is
+// looked up once per device (hipGetSymbolAddress, with that device current)
+// and only that address is handed to kernels. The fused split and the
+// combine use the plan and the partial slots of the workspace: the plan is
+// written by the split before the combine reads it, and every partial the
+// combine reads was written by the split of the same call, so nothing has to
+// start at zero. Calls that overlap on one GPU share the array and race.
+
+namespace gkv {
+constexpr int kScratchWorkgroups = 512; // ranges (split workgroups) the scratch holds
+constexpr size_t kScratchBytes =
+    ((((size_t)(kPlanHeader + kMaxBatch + 1) * 4 + 255) & ~(size_t)255) +
+     (size_t)kPartsPerRange * kScratchWorkgroups * 8 * (kPartFloats + kMlStride) * 4 + 255) &
+    ~(size_t)255;
+static __device__ __align__(256) char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+
+// The scratch array's device address on the current device (looked up on the
+// first call on that device), or nullptr with the HIP error recorded.
+static void *scratch_ptr() {
+  static std::mutex mu;
+  static void *ptrs[kMaxDevices] = {};
+  int dev = 0;
+  if (hip_status(hipGetDevice(&dev), "hipGetDevice") != GKV_OK)
+    return nullptr;
+  if (dev < 0 || dev >= kMaxDevices)
+    return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void *p = nullptr;
+    if (hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress") !=
+        GKV_OK)
+      return nullptr;
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
+}
+} // namespace gkv
+
+extern "C" int gkv_decode_layer_noalloc(void *stream, int32_t B, int32_t n_q_heads,
+                                        const float *qkv, int64_t row_stride,
+                                        const float *cos_tab, const float *sin_tab,
+                                        const int32_t *seq_lens, int32_t max_seq_len,
+                                        gkv_cache_view cache, int32_t window, const float *sinks,
+                                        void *out, int64_t out_stride, int32_t out_dtype,
+                                        uint32_t *dev_err) {
+  if (cache.n_kv_heads > 8 || B > kMaxBatch)
+    return GKV_ERR_CAPACITY; // the scratch is sized for 8 kv heads and kMaxBatch sequences
+  void *ws = scratch_ptr();
+  if (!ws)
+    return GKV_ERR_HIP;
+  DecodeArgs a;
+  AppendArgs ap;
+  int st = prepare(a, B, n_q_heads, qkv, row_stride, cos_tab, sin_tab, seq_lens, max_seq_len,
+                   cache, window, sinks, 0, ws, kScratchBytes, out, out_stride, out_dtype,
+                   dev_err, true, kScratchWorkgroups, false);
+  if (st == GKV_OK)
+    st = layer_append_args(ap, B, n_q_heads, qkv, row_stride, cos_tab, sin_tab, seq_lens, cache,
+                           dev_err);
+  if (st != GKV_OK || B == 0)
+    return st;
+  if ((st = launch_fused(a, &ap, (hipStream_t)stream)))
+    return st;
+  return launch_combine(a, (hipStream_t)stream);
+}

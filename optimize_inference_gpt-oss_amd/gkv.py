@@ -94,6 +94,8 @@ SIGNATURES = {
     "gkv_decode_layer": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
                                         CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
                                         _vp]),
+    "gkv_decode_layer_noalloc": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
+                                               CacheView, _i32, _vp, _vp, _i64, _i32, _vp]),
     "gkv_decode_layer_split": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
                                         CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
                                         _vp]),
@@ -280,6 +282,18 @@ def decode_layer(qkv, seq_lens, max_seq_len, view: CacheView, sinks, out, cos_ta
     decode_attention(qkv, seq_lens, max_seq_len, view, sinks, out, window=window,
                      cos_tab=cos_tab, sin_tab=sin_tab, split_tokens=split_tokens,
                      workspace=workspace, dev_err=dev_err, stream=stream, stage="layer")
+
+
+def decode_layer_noalloc(qkv, seq_lens, max_seq_len, view: CacheView, sinks, out, cos_tab,
+                         sin_tab, window=0, dev_err=None, stream=None):
+    """gkv_decode_layer_noalloc: gkv_decode_layer on the library's own scratch."""
+    import torch
+    out_dtype = BF16 if out.dtype == torch.bfloat16 else F32
+    st = lib().gkv_decode_layer_noalloc(stream_handle(stream), qkv.shape[0], sinks.shape[0],
+                                        ptr(qkv), qkv.stride(0), ptr(cos_tab), ptr(sin_tab),
+                                        ptr(seq_lens), max_seq_len, view, window, ptr(sinks),
+                                        ptr(out), out.stride(0), out_dtype, ptr(dev_err))
+    check("gkv_decode_layer_noalloc", st)
 
 
 def prefill_attention(cu_seqlens, max_len, q, k, v, sinks, out, n_kv_heads, window=0,
