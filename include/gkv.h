@@ -22,9 +22,11 @@
  *   gkv_decode_prepare, gkv_decode_split, gkv_decode_combine
  *                         <- the per-wave split and the LDS merge inside
  *                            attention_gqa8_kernel, fast_attention.hpp:164-425 (a7: 383-424)
- *   gkv_prefill_attention <- no reference kernel; the reference feeds prompts one
- *                            token at a time through the decode step
- *                            (gpu_engine.hpp:811-813); same semantics per position
+ *   gkv_prefill_attention, gkv_prefill_paged
+ *                         <- no reference kernel; the reference feeds prompts one
+ *                            token at a time through the decode step, each
+ *                            attending to the cache (gpu_engine.hpp:805-823); same
+ *                            semantics per position
  *   gkv_pool_*            <- KV allocation in gpu_alloc_state, gpu_engine.hpp:306-334,
  *                            and its sizing/regrow (gpu_fit_batch :425-433, :921-927)
  *
@@ -65,6 +67,9 @@ typedef enum {
  * (they never fault on it: the token is treated as absent). */
 #define GKV_DEVERR_BLOCK_ID 1u /* a table entry outside [0, num_blocks) */
 #define GKV_DEVERR_LENGTH 2u   /* a sequence length beyond the table's capacity */
+#define GKV_DEVERR_ALIGN 4u    /* a prefill start position that is not a multiple of 16 */
+#define GKV_DEVERR_RANGE 8u    /* a V beyond the prefill's range (|v| >= 2^26: the output
+                                  holds inf there) */
 
 typedef enum { GKV_F32 = 0, GKV_BF16 = 1 } gkv_dtype;
 
@@ -267,12 +272,35 @@ int gkv_decode_layer_noalloc(void *stream, int32_t B, int32_t n_q_heads, const f
  * q, k, v and the tables are 16-byte aligned, q_stride a multiple of 4
  * (GKV_ERR_ARG otherwise). V enters an fp16 matrix core as v * 2^-10: exact
  * for bf16 magnitudes 2^-4 .. 2^26, an absolute error of at most 2^-15 below,
- * inf above (which the output shows). */
+ * inf above (which the output shows; gkv_prefill_paged also flags it). */
 int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_seqlens, int32_t max_len,
                           int32_t n_q_heads, int32_t n_kv_heads, const float *q,
                           int64_t q_stride, const float *cos_tab, const float *sin_tab,
                           const void *k, const void *v, const float *sinks, int32_t window,
                           void *out, int64_t out_stride, int32_t out_dtype);
+
+/* Causal attention of prompt chunks that continue sequences already in the
+ * paged cache (chunked prefill), same semantics: row j of prompt b is position
+ * start_pos[b] + j and attends to positions max(0, p - W + 1) .. p, plus the
+ * sink. start_pos: device int32 [B], multiples of 16 (else GKV_DEVERR_ALIGN
+ * and the rows attend to themselves only), or NULL (all 0).
+ *   keys before start_pos[b]  from the cache (gkv_cache_view, bf16 V): the
+ *            full layer's table, or a ring of W slots (cache.ring == window),
+ *            which must still hold them -- append a ring layer's chunk after
+ *            this call
+ *   keys from start_pos[b] on  from the packed rows k, v (bf16 [rows][Hkv][64],
+ *            gkv_kv_append's k_pack/v_pack of this chunk); k = v = NULL
+ *            (these keys from the cache as well) returns GKV_ERR_UNSUPPORTED
+ *   dev_err  NULL, or a device uint32 that gets GKV_DEVERR_* bits (block ids
+ *            outside the pool, misaligned start positions, V out of range)
+ * The other arguments are gkv_prefill_attention's; cos/sin rows are taken at
+ * the rows' positions. */
+int gkv_prefill_paged(void *stream, int32_t B, const int32_t *cu_seqlens,
+                      const int32_t *start_pos, int32_t max_len, int32_t n_q_heads,
+                      const float *q, int64_t q_stride, const float *cos_tab,
+                      const float *sin_tab, const void *k, const void *v, gkv_cache_view cache,
+                      const float *sinks, int32_t window, void *out, int64_t out_stride,
+                      int32_t out_dtype, uint32_t *dev_err);
 
 /* ---- Paged KV pool (host bookkeeping, device storage) -------------------- */
 

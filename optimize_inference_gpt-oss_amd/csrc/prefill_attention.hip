@@ -30,13 +30,27 @@
 // with the sink, and the sink added in the final normalisation, as in the
 // decode kernel. The row sums are fp32 sums of the same fp16 weights.
 //
+// Chunks after a history: a prompt's rows may continue a sequence that
+// already holds start_pos[b] tokens (a multiple of 16) in the paged cache.
+// Row j is then position start + j and attends to positions
+// max(0, start + j - W + 1) .. start + j: those before start come from the
+// cache (the full layer's table, or the ring of W slots, which must still
+// hold them: append a ring layer's chunk after this call), those from start
+// on from the packed rows (or also from the cache, when no packed rows are
+// given: a full layer whose chunk was appended first).
+//
 // LDS (66 KB, two workgroups per CU): a pipeline of 3 K/V tile stages of 64
-// keys, fed by direct-to-LDS loads 2 tiles ahead (K and V rows as they are in
-// memory, 16-byte slots XOR-swizzled per key row); the V of tile t + 1 is
-// turned into V^T [64 dims][64 keys + 8 pad] fp16 while tile t is computed,
-// into the other of two V^T buffers, so a tile needs one barrier.
+// keys, fed by direct-to-LDS loads 2 tiles ahead. Each 16-key group of a tile
+// is one paged block's 2 KB (from the cache), staged in its block layout (a
+// lane's K operand is then one 16-byte read at lane * 16), or 16 packed rows,
+// staged as rows with 16-byte slots XOR-swizzled per key row (conflict-free
+// operand reads without padding). The V of tile t + 1 is turned into V^T [64 dims][64 keys + 8 pad]
+// fp16 while tile t is computed, into the other of two V^T buffers, so a tile
+// needs one barrier.
 #include "gkv_device.hpp"
 #include "lds_dma.hpp"
+
+#include <climits>
 
 namespace gkv {
 
@@ -49,19 +63,27 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 struct PrefillArgs {
   const int32_t *cu;
+  const int32_t *start;           // per prompt: tokens already cached (nullptr: none)
   const float *q;
   int64_t q_stride;
-  const float *cos_tab, *sin_tab; // nullptr: q is rotated; else rotate row j at position j
-  const uint16_t *k, *v;
+  const float *cos_tab, *sin_tab; // nullptr: q is rotated; else rotate row j at its position
+  const uint16_t *k, *v;          // packed rows (nullptr: every key from the cache)
   int64_t kv_stride; // elements per packed row: Hkv * 64
+  const uint16_t *kc, *vc;        // the paged cache (K and V block layouts)
+  const int32_t *table;
+  int table_stride, num_blocks, ring;
   const float *sinks;
   int B, G, n_kv_heads, window, n_qblocks;
   void *out;
   int64_t out_stride;
   int out_bf16;
+  uint32_t *dev_err;
 };
 
-template <int NW>
+// HIST: prompts may continue a cached history (start positions, keys from
+// the cache); without it every key comes from the packed rows and the
+// history paths are compiled out.
+template <int NW, bool HIST>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8 ? 4 : 1))) void prefill_kernel(PrefillArgs a) {
   constexpr int D = kHeadDim;
   constexpr int NT = NW * 64;
@@ -88,11 +110,20 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   const int q0 = qb * kQBlock;
   if (q0 >= L)
     return;
-  const int q_last = min(q0 + kQBlock, L) - 1;
+  int start = HIST && a.start ? a.start[b] : 0; // position of row 0
+  if (HIST && (start < 0 || (start & (kBlockTokens - 1)) != 0)) {
+    if (threadIdx.x == 0 && a.dev_err)
+      atomicOr(a.dev_err, GKV_DEVERR_ALIGN);
+    start = 0; // the rows then attend to themselves only
+  }
+  // positions from here on: queries p0 .. p_last, keys k_lo .. p_last
+  const int p0 = start + q0, p_last = start + min(q0 + kQBlock, L) - 1;
   const int W = a.window;
-  int k_lo = W > 0 ? max(0, q0 - W + 1) : 0;
+  int k_lo = W > 0 ? max(0, p0 - W + 1) : 0;
   k_lo &= ~(kKTile - 1);
-  const int n_tiles = (q_last + 1 - k_lo + kKTile - 1) / kKTile;
+  const int n_tiles = (p_last + 1 - k_lo + kKTile - 1) / kKTile;
+  // keys before this position come from the cache
+  const int hist_end = !HIST ? 0 : a.k ? start : INT_MAX;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -113,16 +144,53 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   auto v_stage = [&](int st) -> uint16_t * {
     return st == 0 ? v_st0 : st == 1 ? v_st1 : v_st2;
   };
+  // The block id of the cached 16-key group at position p (wave-uniform:
+  // read through the scalar cache). An id outside the pool is flagged and
+  // replaced by block 0 (finite data; the output of that prompt is then
+  // meaningless, and the error word says so).
+  typedef const __attribute__((address_space(4))) int32_t *ConstI32;
+  auto cached_block = [&](int p) -> int64_t {
+    const int grp = (W > 0 && a.ring > 0 ? p % a.ring : p) / kBlockTokens;
+    int id = -1;
+    if (grp < a.table_stride)
+      id = ((ConstI32)a.table)[(int64_t)b * a.table_stride + grp];
+    id = uniform(id);
+    if (id < 0 || id >= a.num_blocks) {
+      if (lane == 0 && a.dev_err)
+        atomicOr(a.dev_err, GKV_DEVERR_BLOCK_ID);
+      id = 0;
+    }
+    return ((int64_t)id * a.n_kv_heads + g) * (kBlockTokens * D);
+  };
+  // Tile t into stage st: 16 loads of 1 KB (4 groups x K/V x 2 halves), each
+  // wave 16 / NW of them. Every slot issues its loads (packed rows past the
+  // prompt clamped, tiles past the last re-read), so the number of loads that
+  // follow a tile's is fixed and the wait below is exact.
   auto dma = [&](int t, int st) {
     const int kt0 = k_lo + t * kKTile;
 #pragma unroll
-    for (int i = 0; i < 8 / NW; i++) {
-      const int chunk = wave + i * NW;
-      const int key = chunk * 8 + (lane >> 3), slot = lane & 7;
-      const int row = row0 + min(kt0 + key, L - 1);
-      const int64_t off = (int64_t)row * a.kv_stride + g * D + 8 * (slot ^ (key & 7));
-      dma16(a.k + off, k_stage(st) + chunk * 512);
-      dma16(a.v + off, v_stage(st) + chunk * 512);
+    for (int i = 0; i < 16 / NW; i++) {
+      const int ins = wave + i * NW;
+      const int is_v = ins >> 3, grp = (ins >> 1) & 3, half = ins & 1;
+      const int p = kt0 + kBlockTokens * grp; // first position of the group
+      uint16_t *dst = (is_v ? v_stage(st) : k_stage(st)) + grp * 1024 + half * 512;
+      // a wave-uniform base and this lane's element offset from it
+      const uint16_t *src;
+      uint32_t off;
+      if (HIST && p < hist_end) {
+        // a cached block: its 2 KB as they are (block layouts); tiles past
+        // the last re-read the last one
+        src = (is_v ? a.vc : a.kc) + cached_block(min(p, p_last)) + half * 512;
+        off = lane * 8;
+      } else {
+        // packed rows (clamped to the prompt's last) as rows: keys 8 half ..
+        // +7 of the group, 16-byte slots swizzled by key % 8
+        const int key = 8 * half + (lane >> 3);
+        const int col = 8 * ((lane & 7) ^ (key & 7));
+        src = (is_v ? a.v : a.k) + (int64_t)row0 * a.kv_stride + g * D;
+        off = (uint32_t)(min(p - start + key, L - 1) * a.kv_stride + col);
+      }
+      dma16(src + off, dst);
     }
   };
   // V of a stage -> V^T as fp16 of v * 2^-10 (exact for bf16 magnitudes
@@ -136,23 +204,52 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
     const _Float16 h = (_Float16)(bf16_to_f32((uint16_t)bits16) * kVScale);
     return (uint32_t)__builtin_bit_cast(uint16_t, h);
   };
-  auto convert_v = [&](int st, int buf) {
+  bool v_range = false; // a V beyond the fp16 range of the staged v * 2^-10
+  auto convert_v = [&](int st, int buf, int t) {
     const uint16_t *vs = v_stage(st);
     uint16_t *vt_w = v_lds + buf * (D * kVRow);
+    const int kt0 = k_lo + t * kKTile;
 #pragma unroll
     for (int i = 0; i < kPieces; i++) {
       const int idx = tid + i * NT;
       const int vw = idx >> 6, ln = idx & 63;
       const int pr = (ln & 15) + 16 * (vw & 1), pd = (ln >> 4) + 4 * (vw >> 1);
       const int r0 = 2 * pr, r1 = 2 * pr + 1;
-      const u32x2 x = *(const u32x2 *)(vs + r0 * D + 8 * ((pd >> 1) ^ (r0 & 7)) + 4 * (pd & 1));
-      const u32x2 y = *(const u32x2 *)(vs + r1 * D + 8 * ((pd >> 1) ^ (r1 & 7)) + 4 * (pd & 1));
+      uint32_t pair[4]; // dims 4pd + j of keys r0 (low half) and r1 (high half)
+      if (HIST && kt0 + (r0 & ~(kBlockTokens - 1)) < hist_end) {
+        // block layout: keys r0, r1 of one dim are adjacent. Slots past the
+        // block's last query position may never have been written: their V
+        // becomes 0 (their weight is 0, and 0 * NaN would not be)
+        const uint16_t *blk = vs + (r0 >> 4) * 1024;
+        const int t0 = r0 & 15;
+        const uint32_t keep = (kt0 + r0 <= p_last ? 0x0000ffffu : 0u) |
+                              (kt0 + r1 <= p_last ? 0xffff0000u : 0u);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int d = 4 * pd + j;
+          pair[j] = keep & *(const uint32_t *)(blk + (d >> 5) * 512 +
+                                               ((t0 >> 2) * 16 + (d & 15)) * 8 +
+                                               ((d >> 4) & 1) * 4 + (t0 & 3));
+        }
+      } else {
+        const u32x2 x = *(const u32x2 *)(vs + r0 * D + 8 * ((pd >> 1) ^ (r0 & 7)) + 4 * (pd & 1));
+        const u32x2 y = *(const u32x2 *)(vs + r1 * D + 8 * ((pd >> 1) ^ (r1 & 7)) + 4 * (pd & 1));
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const uint32_t wa = x[j >> 1] >> (16 * (j & 1)), wb = y[j >> 1] >> (16 * (j & 1));
+          pair[j] = (wa & 0xffffu) | (wb << 16);
+        }
+      }
+      bool inf = false;
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const uint32_t wa = x[j >> 1] >> (16 * (j & 1)), wb = y[j >> 1] >> (16 * (j & 1));
-        *(uint32_t *)&vt_w[(4 * pd + j) * kVRow + 2 * pr] =
-            v_half(wa & 0xffffu) | (v_half(wb & 0xffffu) << 16);
+        const uint32_t h0 = v_half(pair[j] & 0xffffu), h1 = v_half(pair[j] >> 16);
+        if (HIST) // the entry point with an error word
+          inf |= (h0 & 0x7fffu) == 0x7c00u || (h1 & 0x7fffu) == 0x7c00u;
+        *(uint32_t *)&vt_w[(4 * pd + j) * kVRow + 2 * pr] = h0 | (h1 << 16);
       }
+      if (HIST)
+        v_range |= __any(inf); // wave-uniform
     }
   };
 
@@ -166,8 +263,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
     f32x4 qr[2][4], cr[2][2], sr[2][2];
 #pragma unroll
     for (int c = 0; c < 2; c++) {
-      const int pos = min(q0 + 16 * c + n, L - 1);
-      const float *qp = a.q + (int64_t)(row0 + pos) * a.q_stride + h * D + 8 * kg;
+      const int j = min(q0 + 16 * c + n, L - 1), pos = start + j;
+      const float *qp = a.q + (int64_t)(row0 + j) * a.q_stride + h * D + 8 * kg;
       // the two halves of RoPE pairs 8kg .. 8kg+7 sit in this lane
       qr[c][0] = *(const f32x4 *)qp;
       qr[c][1] = *(const f32x4 *)(qp + 4);
@@ -225,7 +322,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
     wait_vmcnt<0>();
     lds_barrier();
     dma(t + kStages - 1, (st + kStages - 1) % kStages);
-    convert_v((st + 1) % kStages, (t + 1) & 1);
+    convert_v((st + 1) % kStages, (t + 1) & 1, t + 1);
     const uint16_t *ks = k_stage(st);
     const uint16_t *vt = v_lds + (t & 1) * (D * kVRow);
     const int kt0 = k_lo + t * kKTile;
@@ -234,17 +331,23 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
       const int kb = kt0 + 32 * s; // first key of the step
       // uniform skips: every key after the last query, or (window) older
       // than the first query's window
-      if (!active || kb > q_last || (W > 0 && kb + 31 <= q0 - W))
+      if (!active || kb > p_last || (W > 0 && kb + 31 <= p0 - W))
         continue;
-      const bool need_mask = kb + 31 > q0 || (W > 0 && kb <= q_last - W);
+      const bool need_mask = kb + 31 > p0 || (W > 0 && kb <= p_last - W);
       f32x4 acc[2][2]; // [key tile][query column tile]
 #pragma unroll
       for (int kt = 0; kt < 2; kt++) {
         acc[kt][0] = acc[kt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        // key 16 kt + n of the step (group 2s + kt of the tile), dims
+        // 32dh + 8kg .. +7: in a cached group 16 bytes at lane * 16 of half dh
+        // (block layout), in a packed one slot 4dh + kg of its swizzled row
+        const int kr = 32 * s + 16 * kt + n;
+        const bool blk = HIST && kb + 16 * kt < hist_end;
 #pragma unroll
         for (int dh = 0; dh < 2; dh++) {
-          const int kr = 32 * s + 16 * kt + n; // key row; its dims 32dh + 8kg .. +7
-          const bf16x8 kop = *(const bf16x8 *)&ks[kr * D + 8 * ((4 * dh + kg) ^ (kr & 7))];
+          const int ki = blk ? (2 * s + kt) * 1024 + dh * 512 + lane * 8
+                             : kr * D + 8 * ((4 * dh + kg) ^ (kr & 7));
+          const bf16x8 kop = *(const bf16x8 *)&ks[ki];
 #pragma unroll
           for (int c = 0; c < 2; c++) {
             acc[kt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[c][dh], acc[kt][c], 0, 0, 0);
@@ -265,7 +368,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
           // key ka is kept iff 0 <= qa - ka < W (no window: below 2^31), one
           // unsigned compare per score
           const uint32_t wlim = W > 0 ? (uint32_t)W : 0x80000000u;
-          const int back0 = (q0 + 16 * c + n) - (kb + 4 * kg); // qa - ka of slot 0
+          const int back0 = (p0 + 16 * c + n) - (kb + 4 * kg); // qa - ka of slot 0
 #pragma unroll
           for (int kt = 0; kt < 2; kt++)
 #pragma unroll
@@ -324,7 +427,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   // tile 0's V^T before the loop (tile 1's loads may still fly)
   wait_vmcnt<2 * (8 / NW)>();
   lds_barrier();
-  convert_v(0, 0);
+  convert_v(0, 0, 0);
   for (int t = 0; t < n_tiles; t += kStages) {
     tile(t, 0);
 #pragma unroll
@@ -333,6 +436,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
         tile(t + st, st);
   }
   wait_vmcnt<0>(); // no load may still write into LDS when the workgroup ends
+  if (v_range && lane == 0 && a.dev_err)
+    atomicOr(a.dev_err, GKV_DEVERR_RANGE);
   if (!active)
     return;
 
@@ -365,20 +470,54 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
 
 } // namespace gkv
 
-extern "C" int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_seqlens,
-                                     int32_t max_len, int32_t n_q_heads, int32_t n_kv_heads,
-                                     const float *q, int64_t q_stride, const float *cos_tab,
-                                     const float *sin_tab, const void *k, const void *v,
-                                     const float *sinks, int32_t window, void *out,
-                                     int64_t out_stride, int32_t out_dtype) {
+template <bool HIST>
+static void launch_prefill(const gkv::PrefillArgs &a, int G, dim3 g, hipStream_t s) {
+  using namespace gkv;
+  if (G > 4)
+    hipLaunchKernelGGL((prefill_kernel<8, HIST>), g, dim3(512), 0, s, a);
+  else if (G > 2)
+    hipLaunchKernelGGL((prefill_kernel<4, HIST>), g, dim3(256), 0, s, a);
+  else if (G > 1)
+    hipLaunchKernelGGL((prefill_kernel<2, HIST>), g, dim3(128), 0, s, a);
+  else
+    hipLaunchKernelGGL((prefill_kernel<1, HIST>), g, dim3(64), 0, s, a);
+}
+
+static int prefill_launch(void *stream, int32_t B, const int32_t *cu_seqlens,
+                          const int32_t *start_pos, int32_t max_len, int32_t n_q_heads,
+                          int32_t n_kv_heads, const float *q, int64_t q_stride,
+                          const float *cos_tab, const float *sin_tab, const void *k,
+                          const void *v, const gkv_cache_view *cache, const float *sinks,
+                          int32_t window, void *out, int64_t out_stride, int32_t out_dtype,
+                          uint32_t *dev_err) {
   using namespace gkv;
   if (B < 0 || max_len < 0 || n_q_heads <= 0 || n_kv_heads <= 0 || window < 0 ||
       (out_dtype != GKV_F32 && out_dtype != GKV_BF16))
     return GKV_ERR_ARG;
-  if (B > 0 && (!cu_seqlens || !q || !k || !v || !sinks || !out))
+  if (B > 0 && (!cu_seqlens || !q || !sinks || !out))
     return GKV_ERR_ARG;
-  if (n_q_heads % n_kv_heads != 0 || (cos_tab == nullptr) != (sin_tab == nullptr))
+  if (n_q_heads % n_kv_heads != 0 || (cos_tab == nullptr) != (sin_tab == nullptr) ||
+      (k == nullptr) != (v == nullptr))
     return GKV_ERR_ARG;
+  const bool cached = cache && cache->k; // a history in the cache
+  if (!k && !cached)
+    return GKV_ERR_ARG; // keys from nowhere
+  if (!k)
+    return GKV_ERR_UNSUPPORTED; // chunk keys from the cache: switched off (a GPU memory fault
+                                // in its first test run, cause not yet found)
+  if (start_pos && !cached)
+    return GKV_ERR_ARG; // a history needs the cache
+  if (cached) {
+    if (!cache->v || !cache->block_table || cache->table_stride <= 0 || cache->num_blocks <= 0 ||
+        cache->n_kv_heads != n_kv_heads || cache->ring < 0)
+      return GKV_ERR_ARG;
+    if (cache->v_format != GKV_V_BF16)
+      return GKV_ERR_UNSUPPORTED; // the prefill reads bf16 V
+    if (cache->ring > 0 && (window != cache->ring || !k))
+      return GKV_ERR_ARG; // a ring holds the history only: the chunk comes as packed rows
+    if (((uintptr_t)cache->k | (uintptr_t)cache->v) % 16 != 0)
+      return GKV_ERR_ARG;
+  }
   const int G = n_q_heads / n_kv_heads;
   if (G > 8)
     return GKV_ERR_UNSUPPORTED;
@@ -396,6 +535,7 @@ extern "C" int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_
     return GKV_ERR_ARG;
   PrefillArgs a;
   a.cu = cu_seqlens;
+  a.start = start_pos;
   a.q = q;
   a.q_stride = q_stride;
   a.cos_tab = cos_tab;
@@ -403,6 +543,12 @@ extern "C" int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_
   a.k = (const uint16_t *)k;
   a.v = (const uint16_t *)v;
   a.kv_stride = (int64_t)n_kv_heads * kHeadDim;
+  a.kc = cached ? (const uint16_t *)cache->k : nullptr;
+  a.vc = cached ? (const uint16_t *)cache->v : nullptr;
+  a.table = cached ? cache->block_table : nullptr;
+  a.table_stride = cached ? cache->table_stride : 0;
+  a.num_blocks = cached ? cache->num_blocks : 0;
+  a.ring = cached ? cache->ring : 0;
   a.sinks = sinks;
   a.B = B;
   a.G = G;
@@ -412,15 +558,37 @@ extern "C" int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_
   a.out = out;
   a.out_stride = out_stride;
   a.out_bf16 = out_dtype == GKV_BF16;
+  a.dev_err = dev_err;
   hipStream_t s = (hipStream_t)stream;
   const dim3 g((unsigned)grid);
-  if (G > 4)
-    hipLaunchKernelGGL(prefill_kernel<8>, g, dim3(512), 0, s, a);
-  else if (G > 2)
-    hipLaunchKernelGGL(prefill_kernel<4>, g, dim3(256), 0, s, a);
-  else if (G > 1)
-    hipLaunchKernelGGL(prefill_kernel<2>, g, dim3(128), 0, s, a);
+  if (cached)
+    launch_prefill<true>(a, G, g, s);
   else
-    hipLaunchKernelGGL(prefill_kernel<1>, g, dim3(64), 0, s, a);
+    launch_prefill<false>(a, G, g, s);
   return launch_status("prefill_kernel");
+}
+
+extern "C" int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_seqlens,
+                                     int32_t max_len, int32_t n_q_heads, int32_t n_kv_heads,
+                                     const float *q, int64_t q_stride, const float *cos_tab,
+                                     const float *sin_tab, const void *k, const void *v,
+                                     const float *sinks, int32_t window, void *out,
+                                     int64_t out_stride, int32_t out_dtype) {
+  if (!k || !v)
+    return GKV_ERR_ARG;
+  return prefill_launch(stream, B, cu_seqlens, nullptr, max_len, n_q_heads, n_kv_heads, q,
+                        q_stride, cos_tab, sin_tab, k, v, nullptr, sinks, window, out, out_stride,
+                        out_dtype, nullptr);
+}
+
+extern "C" int gkv_prefill_paged(void *stream, int32_t B, const int32_t *cu_seqlens,
+                                 const int32_t *start_pos, int32_t max_len, int32_t n_q_heads,
+                                 const float *q, int64_t q_stride, const float *cos_tab,
+                                 const float *sin_tab, const void *k, const void *v,
+                                 gkv_cache_view cache, const float *sinks, int32_t window,
+                                 void *out, int64_t out_stride, int32_t out_dtype,
+                                 uint32_t *dev_err) {
+  return prefill_launch(stream, B, cu_seqlens, start_pos, max_len, n_q_heads, cache.n_kv_heads,
+                        q, q_stride, cos_tab, sin_tab, k, v, &cache, sinks, window, out,
+                        out_stride, out_dtype, dev_err);
 }

@@ -22,6 +22,8 @@ GKV_ERR_HIP = -5
 GKV_ERR_WORKSPACE = -6
 DEVERR_BLOCK_ID = 1
 DEVERR_LENGTH = 2
+DEVERR_ALIGN = 4
+DEVERR_RANGE = 8
 F32 = 0
 BF16 = 1
 
@@ -109,6 +111,8 @@ SIGNATURES = {
                                           _vp, _sz, _vp, _i64, _i32]),
     "gkv_prefill_attention": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i32, _i32, _vp, _i64, _vp,
                                              _vp, _vp, _vp, _vp, _i32, _vp, _i64, _i32]),
+    "gkv_prefill_paged": (ctypes.c_int, [_vp, _i32, _vp, _vp, _i32, _i32, _vp, _i64, _vp, _vp,
+                                         _vp, _vp, CacheView, _vp, _i32, _vp, _i64, _i32, _vp]),
     "gkv_pool_create": (ctypes.c_int, [ctypes.POINTER(PoolConfig), ctypes.POINTER(_vp)]),
     "gkv_pool_destroy": (ctypes.c_int, [_vp]),
     "gkv_pool_seq_alloc": (ctypes.c_int, [_vp, ctypes.POINTER(_i32)]),
@@ -307,6 +311,20 @@ def prefill_attention(cu_seqlens, max_len, q, k, v, sinks, out, n_kv_heads, wind
                                      ptr(v), ptr(sinks), window, ptr(out), out.stride(0),
                                      out_dtype)
     check("gkv_prefill_attention", st)
+
+
+def prefill_paged(cu_seqlens, max_len, q, cache: CacheView, sinks, out, start_pos=None, k=None,
+                  v=None, window=0, cos_tab=None, sin_tab=None, dev_err=None, stream=None):
+    """gkv_prefill_paged: chunks continuing the sequences in `cache` (start_pos
+    tokens each, multiples of 16); the chunk's keys from the packed rows k, v,
+    or from the cache when they are None."""
+    import torch
+    out_dtype = BF16 if out.dtype == torch.bfloat16 else F32
+    st = lib().gkv_prefill_paged(stream_handle(stream), cu_seqlens.shape[0] - 1, ptr(cu_seqlens),
+                                 ptr(start_pos), max_len, sinks.shape[0], ptr(q), q.stride(0),
+                                 ptr(cos_tab), ptr(sin_tab), ptr(k), ptr(v), cache, ptr(sinks),
+                                 window, ptr(out), out.stride(0), out_dtype, ptr(dev_err))
+    check("gkv_prefill_paged", st)
 
 
 class Pool:

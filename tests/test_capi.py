@@ -200,3 +200,21 @@ def test_pool_calls_reject_null_and_bad_config(gkv):
         cfg.update(bad)
         st = lib.gkv_pool_create(ctypes.byref(gkv.PoolConfig(*cfg.values())), ctypes.byref(h))
         assert st in (gkv.GKV_ERR_ARG, gkv.GKV_ERR_UNSUPPORTED), (bad, st)
+
+
+def test_prefill_paged_argument_checks(gkv):
+    L = gkv.lib()
+    fake = 0x1000  # never dereferenced: the checks fail first
+    def call(view=None, k=fake, v=fake, start=fake, window=0, B=2):
+        return L.gkv_prefill_paged(None, B, fake, start, 100, 64, fake, 80 * 64, fake, fake, k, v,
+                                   view if view is not None else _view(gkv, k=fake, v=fake), fake,
+                                   window, fake,
+                                   64 * 64, 0, None)
+    assert call(B=-1) == gkv.GKV_ERR_ARG
+    assert call(k=None, v=None) == gkv.GKV_ERR_UNSUPPORTED  # chunk keys from the cache: off
+    assert call(v=None) == gkv.GKV_ERR_ARG                  # one of k, v
+    assert call(view=_view(gkv, k=None, v=None)) == gkv.GKV_ERR_ARG  # a history needs the cache
+    assert call(view=_view(gkv, k=fake, v=fake, ring=128), window=0) == gkv.GKV_ERR_ARG
+    assert call(view=_view(gkv, k=fake, v=fake, ring=128), window=64) == gkv.GKV_ERR_ARG
+    assert call(view=_view(gkv, k=fake, v=fake, v_format=1)) == gkv.GKV_ERR_UNSUPPORTED
+    assert call(B=0) == gkv.GKV_OK

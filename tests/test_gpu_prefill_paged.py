@@ -1,0 +1,199 @@
+"""GPU parity of chunked prefill over a paged history (gkv_prefill_paged).
+
+Each prompt is fed in two chunks. Chunk 1 (positions 0 .. C-1, C a multiple
+of 16) is appended into the paged cache and attended to with start 0; chunk 2
+(positions C .. L-1) attends to the history C tokens from the cache and to
+itself. Every output row is compared with the one-shot oracle prefill of the
+whole prompt (orc_prefill_attention: the reference's decode attention at
+every position, run.cpp:597-642) within max-abs 2e-3 + rel 1e-2.
+
+- Full layer, chunk 2's keys from its packed rows (history from the cache).
+- Full layer, chunk 2 appended first and every key from the cache (skipped:
+  that mode is switched off, GKV_ERR_UNSUPPORTED).
+- Ring layer (window 128): chunk 2 attended before it is appended (the ring
+  still holds the last 128 positions of chunk 1), then appended.
+- Error words: a start that is not a multiple of 16, and a V beyond the
+  prefill's range.
+"""
+import numpy as np
+import pytest
+
+from kvcase import allclose_report
+
+pytestmark = pytest.mark.gpu
+
+D = 64
+
+
+class Chunked:
+    def __init__(self, torch, gkv, oracle, L, C, Hq=64, Hkv=8, window=0, seed=0, scale=0.5):
+        rng = np.random.default_rng(seed)
+        self.torch, self.gkv = torch, gkv
+        self.L = np.asarray(L, np.int32)
+        self.C = np.asarray(C, np.int32)
+        assert np.all(self.C % 16 == 0) and np.all(self.C <= self.L)
+        self.B, self.Hq, self.Hkv, self.window = len(L), Hq, Hkv, window
+        cu = np.concatenate([[0], np.cumsum(self.L)]).astype(np.int32)
+        T = int(cu[-1])
+        self.qkv = (rng.standard_normal((T, (Hq + 2 * Hkv) * D)) * scale).astype(np.float32)
+        self.sinks = rng.standard_normal(Hq).astype(np.float32)
+        pos = np.concatenate([np.arange(n) for n in self.L]).astype(np.int32)
+        cos, sin = oracle.rope_table(int(self.L.max()))
+        q_rot, _, kb, vb = oracle.kv_append(self.qkv, Hq, Hkv, cos, sin, pos)
+        self.ref = oracle.prefill_attention(cu, q_rot, oracle.from_bf16(kb), oracle.from_bf16(vb),
+                                            self.sinks, window=window)
+        self.cu_all, self.pos = cu, pos
+        # the pool: one layer (a ring layer when window > 0), NaN in every slot
+        self.pool = gkv.Pool(n_layers=1, n_kv_heads=Hkv, max_seqs=self.B,
+                             max_seq_len=int(self.L.max()), window=window,
+                             num_blocks=int(((self.L + 15) // 16).sum()) + 8,
+                             shuffle_seed=seed + 3)
+        for b in range(self.B):
+            assert self.pool.seq_alloc() == b
+            assert self.pool.reserve(b, int(self.L[b])) == 0
+        self.pool.sync()
+        self.view = self.pool.view(0)
+        n = self.view.num_blocks * Hkv * 16 * D
+        nan = torch.full((n,), -1, dtype=torch.int16, device="cuda")  # bf16 0xffff: NaN
+        for base in (self.view.k, self.view.v):
+            gkv.hip_memcpy_d2d(base, nan.data_ptr(), n * 2)
+        torch.cuda.synchronize()
+        t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to("cuda")  # noqa: E731
+        self.t = t
+        self.cos_d, self.sin_d = t(cos), t(sin)
+        self.sinks_d = t(self.sinks)
+
+    def chunk_rows(self, which):
+        """Rows (indices into the whole-prompt arrays) of chunk 1 or 2, prompt by prompt."""
+        rows, cu = [], [0]
+        for b in range(self.B):
+            lo, hi = (0, self.C[b]) if which == 1 else (self.C[b], self.L[b])
+            rows.append(np.arange(self.cu_all[b] + lo, self.cu_all[b] + hi))
+            cu.append(cu[-1] + hi - lo)
+        return np.concatenate(rows).astype(np.int64), np.asarray(cu, np.int32)
+
+    def append(self, which, err):
+        """The chunk's rows into the cache; the lengths after it (C or L) tell
+        a ring which rows it keeps."""
+        rows, cu = self.chunk_rows(which)
+        seq = np.repeat(np.arange(self.B), np.diff(cu)).astype(np.int32)
+        lens = self.C if which == 1 else self.L
+        self.gkv.kv_append(self.t(self.qkv[rows]), self.Hq, self.cos_d, self.sin_d,
+                           self.t(self.pos[rows]), self.view, row_seq=self.t(seq),
+                           seq_lens=self.t(lens), dev_err=err)
+
+    def packed(self, which):
+        """The chunk's packed bf16 K/V rows (gkv_kv_append with no cache)."""
+        torch = self.torch
+        rows, _ = self.chunk_rows(which)
+        n = max(len(rows), 1)
+        kp = torch.zeros((n, self.Hkv * D), dtype=torch.int16, device="cuda")
+        vp = torch.zeros((n, self.Hkv * D), dtype=torch.int16, device="cuda")
+        none = self.gkv.CacheView(None, None, None, 0, 0, self.Hkv, 0)
+        self.gkv.kv_append(self.t(self.qkv[rows]), self.Hq, self.cos_d, self.sin_d,
+                           self.t(self.pos[rows]), none, k_pack=kp, v_pack=vp)
+        return kp, vp
+
+    def prefill(self, which, err, k=None, v=None, start=None):
+        torch = self.torch
+        rows, cu = self.chunk_rows(which)
+        if start is None:
+            start = np.zeros(self.B, np.int32) if which == 1 else self.C
+        out = torch.full((max(len(rows), 1), self.Hq * D), float("nan"), dtype=torch.float32,
+                         device="cuda")
+        self.gkv.prefill_paged(self.t(cu), int(np.diff(cu).max()), self.t(self.qkv[rows]),
+                               self.view, self.sinks_d, out, start_pos=self.t(start.astype(np.int32)),
+                               k=k, v=v, window=self.window, cos_tab=self.cos_d,
+                               sin_tab=self.sin_d, dev_err=err)
+        torch.cuda.synchronize()
+        return out.cpu().numpy()[:len(rows)].reshape(len(rows), self.Hq, D), rows
+
+    def check(self, got, rows, what):
+        bad, worst = allclose_report(got, self.ref[rows])
+        assert bad == 0, f"{what}: {bad} outputs out of tolerance (max err {worst:.3e})"
+        return worst
+
+
+LENS = [300, 517, 64, 130, 1040, 33]
+CUTS = [128, 256, 48, 128, 512, 16]
+
+
+@pytest.mark.parametrize("cache_only", [
+    False,
+    pytest.param(True, marks=pytest.mark.skip(
+        reason="chunk keys from the cache: its first GPU run faulted the GPU; the entry point "
+               "returns GKV_ERR_UNSUPPORTED for it until the cause is found")),
+])
+def test_two_chunks_full_layer(oracle, gkv, cuda, cache_only):
+    import torch
+    c = Chunked(torch, gkv, oracle, LENS, CUTS, seed=11)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    try:
+        kp, vp = c.packed(1)
+        c.append(1, err)
+        got, rows = c.prefill(1, err, k=kp, v=vp)
+        w1 = c.check(got, rows, "chunk 1")
+        if cache_only:
+            c.append(2, err)                      # chunk 2 into the cache first
+            got, rows = c.prefill(2, err)         # every key from the cache
+        else:
+            kp, vp = c.packed(2)
+            got, rows = c.prefill(2, err, k=kp, v=vp)  # history from the cache
+            c.append(2, err)
+        w2 = c.check(got, rows, "chunk 2")
+        assert int(err.item()) == 0
+        print(f"full layer cache_only={cache_only}: max abs err {w1:.2e} / {w2:.2e}")
+    finally:
+        c.pool.close()
+
+
+def test_two_chunks_ring_layer(oracle, gkv, cuda):
+    """Window 128 on a ring of 128 slots: chunk 2 attends to the ring's
+    history before its own append overwrites it."""
+    import torch
+    c = Chunked(torch, gkv, oracle, [400, 700, 96, 260], [256, 512, 32, 128], window=128,
+                seed=12)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    try:
+        kp, vp = c.packed(1)
+        got, rows = c.prefill(1, err, k=kp, v=vp)
+        c.append(1, err)
+        c.check(got, rows, "chunk 1")
+        kp, vp = c.packed(2)
+        got, rows = c.prefill(2, err, k=kp, v=vp)
+        c.append(2, err)
+        c.check(got, rows, "chunk 2")
+        assert int(err.item()) == 0
+    finally:
+        c.pool.close()
+
+
+def test_start_not_a_block_multiple_is_flagged(oracle, gkv, cuda):
+    import torch
+    c = Chunked(torch, gkv, oracle, [100, 80], [32, 48], seed=13)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    try:
+        c.append(1, err)
+        kp, vp = c.packed(2)
+        got, _ = c.prefill(2, err, k=kp, v=vp, start=np.array([32, 40], np.int32))
+        assert int(err.item()) & gkv.DEVERR_ALIGN
+        assert np.isfinite(got).all()
+    finally:
+        c.pool.close()
+
+
+def test_v_beyond_range_is_flagged(oracle, gkv, cuda):
+    """|v| >= 2^26 leaves the fp16 range of the staged v * 2^-10: the error
+    word says so (the output holds inf there)."""
+    import torch
+    c = Chunked(torch, gkv, oracle, [64], [32], seed=14)
+    Hq, Hkv = c.Hq, c.Hkv
+    c.qkv[40, (Hq + Hkv) * D + 5] = 2.0 ** 27  # chunk 2, V of kv head 0, dim 5
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    try:
+        c.append(1, err)
+        kp, vp = c.packed(2)
+        c.prefill(2, err, k=kp, v=vp)
+        assert int(err.item()) & gkv.DEVERR_RANGE
+    finally:
+        c.pool.close()
