@@ -289,8 +289,8 @@ int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_seqlens, in
  *            which must still hold them -- append a ring layer's chunk after
  *            this call
  *   keys from start_pos[b] on  from the packed rows k, v (bf16 [rows][Hkv][64],
- *            gkv_kv_append's k_pack/v_pack of this chunk); k = v = NULL
- *            (these keys from the cache as well) returns GKV_ERR_UNSUPPORTED
+ *            gkv_kv_append's k_pack/v_pack of this chunk); k = v = NULL: from
+ *            the cache as well (a full layer whose chunk was appended first)
  *   dev_err  NULL, or a device uint32 that gets GKV_DEVERR_* bits (block ids
  *            outside the pool, misaligned start positions, V out of range)
  * The other arguments are gkv_prefill_attention's; cos/sin rows are taken at

@@ -502,9 +502,6 @@ static int prefill_launch(void *stream, int32_t B, const int32_t *cu_seqlens,
   const bool cached = cache && cache->k; // a history in the cache
   if (!k && !cached)
     return GKV_ERR_ARG; // keys from nowhere
-  if (!k)
-    return GKV_ERR_UNSUPPORTED; // chunk keys from the cache: switched off (a GPU memory fault
-                                // in its first test run, cause not yet found)
   if (start_pos && !cached)
     return GKV_ERR_ARG; // a history needs the cache
   if (cached) {

@@ -211,7 +211,7 @@ def test_prefill_paged_argument_checks(gkv):
                                    window, fake,
                                    64 * 64, 0, None)
     assert call(B=-1) == gkv.GKV_ERR_ARG
-    assert call(k=None, v=None) == gkv.GKV_ERR_UNSUPPORTED  # chunk keys from the cache: off
+    assert call(k=None, v=None, view=_view(gkv, k=None, v=None)) == gkv.GKV_ERR_ARG  # no keys
     assert call(v=None) == gkv.GKV_ERR_ARG                  # one of k, v
     assert call(view=_view(gkv, k=None, v=None)) == gkv.GKV_ERR_ARG  # a history needs the cache
     assert call(view=_view(gkv, k=fake, v=fake, ring=128), window=0) == gkv.GKV_ERR_ARG

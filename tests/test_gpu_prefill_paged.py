@@ -8,8 +8,8 @@ whole prompt (orc_prefill_attention: the reference's decode attention at
 every position, run.cpp:597-642) within max-abs 2e-3 + rel 1e-2.
 
 - Full layer, chunk 2's keys from its packed rows (history from the cache).
-- Full layer, chunk 2 appended first and every key from the cache (skipped:
-  that mode is switched off, GKV_ERR_UNSUPPORTED).
+- Full layer, chunk 2 appended first and every key from the cache (also the
+  load slots past the block's last tile: they re-read cached blocks).
 - Ring layer (window 128): chunk 2 attended before it is appended (the ring
   still holds the last 128 positions of chunk 1), then appended.
 - Error words: a start that is not a multiple of 16, and a V beyond the
@@ -118,12 +118,7 @@ LENS = [300, 517, 64, 130, 1040, 33]
 CUTS = [128, 256, 48, 128, 512, 16]
 
 
-@pytest.mark.parametrize("cache_only", [
-    False,
-    pytest.param(True, marks=pytest.mark.skip(
-        reason="chunk keys from the cache: its first GPU run faulted the GPU; the entry point "
-               "returns GKV_ERR_UNSUPPORTED for it until the cause is found")),
-])
+@pytest.mark.parametrize("cache_only", [False, True])
 def test_two_chunks_full_layer(oracle, gkv, cuda, cache_only):
     import torch
     c = Chunked(torch, gkv, oracle, LENS, CUTS, seed=11)
