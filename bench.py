@@ -320,15 +320,23 @@ def run_prefill(torch, gkv, args) -> int:
             if record:
                 e[0].record(stream)
             # the append stores K/V (cache + packed rows); Q is rotated by the
-            # prefill as it loads the qkv rows
+            # prefill as it loads the qkv rows. --prefill-from-cache: a full
+            # layer's append stores the cache only and the prefill reads every
+            # key from it (a ring keeps only the last W positions: packed rows)
+            from_cache = args.prefill_from_cache and not ly["window"]
             gkv.kv_append(ly["qkv"], Hq, cos_d, sin_d, pos_d, ly["view"], row_seq=seq_d,
-                          seq_lens=lens_d, k_pack=ly["k"], v_pack=ly["v"], dev_err=err,
-                          stream=stream)
+                          seq_lens=lens_d, k_pack=None if from_cache else ly["k"],
+                          v_pack=None if from_cache else ly["v"], dev_err=err, stream=stream)
             if record:
                 e[1].record(stream)
-            gkv.prefill_attention(cu_d, max_len, ly["qkv"], ly["k"], ly["v"], ly["sinks"],
-                                  ly["out"], Hkv, window=ly["window"], cos_tab=cos_d,
-                                  sin_tab=sin_d, stream=stream)
+            if from_cache:
+                gkv.prefill_paged(cu_d, max_len, ly["qkv"], ly["view"], ly["sinks"], ly["out"],
+                                  window=0, cos_tab=cos_d, sin_tab=sin_d, dev_err=err,
+                                  stream=stream)
+            else:
+                gkv.prefill_attention(cu_d, max_len, ly["qkv"], ly["k"], ly["v"], ly["sinks"],
+                                      ly["out"], Hkv, window=ly["window"], cos_tab=cos_d,
+                                      sin_tab=sin_d, stream=stream)
             if record:
                 e[2].record(stream)
                 ev.append((li, e))
@@ -511,6 +519,10 @@ def main() -> int:
     ap.add_argument("--separate-append", action="store_true",
                     help="append with gkv_kv_append, then gkv_decode_attention (four launches "
                          "per layer instead of gkv_decode_layer's three)")
+    ap.add_argument("--prefill-from-cache", action="store_true",
+                    help="config 4: the full layer's append writes the paged cache only and the "
+                         "prefill reads every key from it (gkv_prefill_paged) instead of from "
+                         "packed rows")
     ap.add_argument("--staged", action="store_true",
                     help="the staged launches: append fused with the prepare launch (plan, "
                          "block ids, query operands), then the split reading the plan, then the "

@@ -49,6 +49,27 @@ __device__ __forceinline__ void dma16(const void *src, void *l_base) {
                : "memory");
 }
 
+// dma16 with a wave-uniform base address (held in SGPRs) and a 32-bit byte
+// offset per lane: no 64-bit address per lane is formed or kept.
+__device__ __forceinline__ void dma16_s(const void *base, uint32_t byte_off, void *l_base) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr)l_base);
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  // (readfirstlane returns a signed int: each half is taken as unsigned
+  // before it is widened, or a low half >= 2^31 would fill the high one)
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint64_t sb = ((uint64_t)hi << 32) | lo;
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\t"
+               "s_mov_b32 m0, %3\n\t"
+               "s_nop 0\n\t"
+               "global_load_lds_dwordx4 %1, %2\n\t"
+               "s_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(byte_off), "s"(sb), "s"(m)
+               : "memory");
+}
+
 // 4 bytes per lane straight into LDS: lane l's dword lands at l_base + 4 l.
 __device__ __forceinline__ void dma4(const void *src, void *l_base) {
   const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr)l_base);

@@ -42,9 +42,11 @@
 // LDS (66 KB, two workgroups per CU): a pipeline of 3 K/V tile stages of 64
 // keys, fed by direct-to-LDS loads 2 tiles ahead. Each 16-key group of a tile
 // is one paged block's 2 KB (from the cache), staged in its block layout (a
-// lane's K operand is then one 16-byte read at lane * 16), or 16 packed rows,
-// staged as rows with 16-byte slots XOR-swizzled per key row (conflict-free
-// operand reads without padding). The V of tile t + 1 is turned into V^T [64 dims][64 keys + 8 pad]
+// lane's K operand is then one 16-byte read at lane * 16), or 16 packed rows.
+// Without a history, packed K and V are staged as rows with 16-byte slots
+// XOR-swizzled per key row (conflict-free operand reads without padding);
+// with one, packed K goes into the block layout too (one operand form), V
+// stays in rows. The V of tile t + 1 is turned into V^T [64 dims][64 keys + 8 pad]
 // fp16 while tile t is computed, into the other of two V^T buffers, so a tile
 // needs one barrier.
 #include "gkv_device.hpp"
@@ -144,17 +146,32 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   auto v_stage = [&](int st) -> uint16_t * {
     return st == 0 ? v_st0 : st == 1 ? v_st1 : v_st2;
   };
-  // The block id of the cached 16-key group at position p (wave-uniform:
-  // read through the scalar cache). An id outside the pool is flagged and
-  // replaced by block 0 (finite data; the output of that prompt is then
-  // meaningless, and the error word says so).
+  // Block ids of the 4 cached groups of a tile (-1: none), read through the
+  // scalar cache (wave-uniform) at the end of the tile before the one whose
+  // loads use them, so the next tile's barrier wait covers their latency. An
+  // id outside the pool is flagged and replaced by block 0 (finite data;
+  // that prompt's output is then meaningless, and the error word says so).
   typedef const __attribute__((address_space(4))) int32_t *ConstI32;
-  auto cached_block = [&](int p) -> int64_t {
-    const int grp = (W > 0 && a.ring > 0 ? p % a.ring : p) / kBlockTokens;
-    int id = -1;
-    if (grp < a.table_stride)
-      id = ((ConstI32)a.table)[(int64_t)b * a.table_stride + grp];
-    id = uniform(id);
+  struct Ids {
+    int v[4];
+  };
+  auto load_ids = [&](int t) -> Ids {
+    Ids r;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      r.v[j] = -1;
+      if (HIST) {
+        const int p = min(k_lo + t * kKTile + kBlockTokens * j, p_last);
+        const int grp = (W > 0 && a.ring > 0 ? p % a.ring : p) / kBlockTokens;
+        if (p < hist_end && grp < a.table_stride)
+          r.v[j] = ((ConstI32)a.table)[(int64_t)b * a.table_stride + grp];
+      }
+    }
+    return r;
+  };
+  auto cached_block = [&](const Ids &ids, int grp) -> int64_t {
+    // a select chain, not an indexed access (which would put the ids in memory)
+    int id = grp == 0 ? ids.v[0] : grp == 1 ? ids.v[1] : grp == 2 ? ids.v[2] : ids.v[3];
     if (id < 0 || id >= a.num_blocks) {
       if (lane == 0 && a.dev_err)
         atomicOr(a.dev_err, GKV_DEVERR_BLOCK_ID);
@@ -166,7 +183,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   // wave 16 / NW of them. Every slot issues its loads (packed rows past the
   // prompt clamped, tiles past the last re-read), so the number of loads that
   // follow a tile's is fixed and the wait below is exact.
-  auto dma = [&](int t, int st) {
+  auto dma = [&](int t, int st, const Ids &ids) {
     const int kt0 = k_lo + t * kKTile;
 #pragma unroll
     for (int i = 0; i < 16 / NW; i++) {
@@ -174,23 +191,39 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
       const int is_v = ins >> 3, grp = (ins >> 1) & 3, half = ins & 1;
       const int p = kt0 + kBlockTokens * grp; // first position of the group
       uint16_t *dst = (is_v ? v_stage(st) : k_stage(st)) + grp * 1024 + half * 512;
-      // a wave-uniform base and this lane's element offset from it
+      // a wave-uniform base and this lane's element offset from it. The lane
+      // index is made opaque here so that the per-lane offsets are formed at
+      // each load rather than hoisted out of the tile loop and kept live
+      // (the history variant has no registers to spare for them)
+      int lane_ = lane;
+      if (HIST)
+        asm volatile("" : "+v"(lane_));
       const uint16_t *src;
       uint32_t off;
       if (HIST && p < hist_end) {
         // a cached block: its 2 KB as they are (block layouts); tiles past
         // the last re-read the last one
-        src = (is_v ? a.vc : a.kc) + cached_block(min(p, p_last)) + half * 512;
-        off = lane * 8;
+        src = (is_v ? a.vc : a.kc) + cached_block(ids, grp) + half * 512;
+        off = lane_ * 8;
+      } else if (HIST && !is_v) {
+        // packed rows (clamped to the prompt's last) into the K block layout,
+        // as a cached block is staged: lane (kg, t) <- dims 32 half + 8 kg ..
+        // +7 of the group's row t
+        src = a.k + (int64_t)row0 * a.kv_stride + g * D;
+        off = (uint32_t)(min(p - start + (lane_ & 15), L - 1) * (int)a.kv_stride + 32 * half +
+                         8 * (lane_ >> 4));
       } else {
         // packed rows (clamped to the prompt's last) as rows: keys 8 half ..
         // +7 of the group, 16-byte slots swizzled by key % 8
-        const int key = 8 * half + (lane >> 3);
-        const int col = 8 * ((lane & 7) ^ (key & 7));
+        const int key = 8 * half + (lane_ >> 3);
+        const int col = 8 * ((lane_ & 7) ^ (key & 7));
         src = (is_v ? a.v : a.k) + (int64_t)row0 * a.kv_stride + g * D;
-        off = (uint32_t)(min(p - start + key, L - 1) * a.kv_stride + col);
+        off = (uint32_t)(min(p - start + key, L - 1) * (int)a.kv_stride + col);
       }
-      dma16(src + off, dst);
+      if (HIST)
+        dma16_s(src, off * 2, dst); // uniform base in SGPRs, 32-bit offsets
+      else
+        dma16(src + off, dst);
     }
   };
   // V of a stage -> V^T as fp16 of v * 2^-10 (exact for bf16 magnitudes
@@ -256,6 +289,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   // ---- query operands: column tile c holds queries q0 + 16c + n; half dh dims 32dh + 8kg + j.
   // The loads of both column tiles (and of their RoPE angles) and of the
   // first K/V tile go out together: one memory round trip before compute.
+  // the block ids of the first tiles go out first
+  const Ids ids0 = load_ids(0), ids1 = load_ids(1);
+  Ids ids_next = load_ids(kStages - 1);
   bf16x8 qhi[2][2], qlo[2][2];
   {
     const float qscale = 0.125f * kLog2e; // 1/sqrt(64); exp -> exp2
@@ -280,7 +316,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
     }
 #pragma unroll
     for (int t = 0; t < kStages - 1; t++)
-      dma(t, t);
+      dma(t, t, t == 0 ? ids0 : ids1);
 #pragma unroll
     for (int c = 0; c < 2; c++) {
       float qv[2][8];
@@ -321,7 +357,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   auto tile = [&](const int t, const int st) {
     wait_vmcnt<0>();
     lds_barrier();
-    dma(t + kStages - 1, (st + kStages - 1) % kStages);
+    dma(t + kStages - 1, (st + kStages - 1) % kStages, ids_next);
     convert_v((st + 1) % kStages, (t + 1) & 1, t + 1);
     const uint16_t *ks = k_stage(st);
     const uint16_t *vt = v_lds + (t & 1) * (D * kVRow);
@@ -339,14 +375,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
       for (int kt = 0; kt < 2; kt++) {
         acc[kt][0] = acc[kt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         // key 16 kt + n of the step (group 2s + kt of the tile), dims
-        // 32dh + 8kg .. +7: in a cached group 16 bytes at lane * 16 of half dh
-        // (block layout), in a packed one slot 4dh + kg of its swizzled row
+        // 32dh + 8kg .. +7: with a history (K staged in the block layout) 16
+        // bytes at lane * 16 of half dh; else slot 4dh + kg of its swizzled row
         const int kr = 32 * s + 16 * kt + n;
-        const bool blk = HIST && kb + 16 * kt < hist_end;
 #pragma unroll
         for (int dh = 0; dh < 2; dh++) {
-          const int ki = blk ? (2 * s + kt) * 1024 + dh * 512 + lane * 8
-                             : kr * D + 8 * ((4 * dh + kg) ^ (kr & 7));
+          const int ki = HIST ? (2 * s + kt) * 1024 + dh * 512 + lane * 8
+                              : kr * D + 8 * ((4 * dh + kg) ^ (kr & 7));
           const bf16x8 kop = *(const bf16x8 *)&ks[ki];
 #pragma unroll
           for (int c = 0; c < 2; c++) {
@@ -423,6 +458,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
           o[c][nn] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vop, ph[c], o[c][nn], 0, 0, 0);
       }
     }
+    // the block ids of the tile whose loads the next tile issues
+    if (HIST)
+      ids_next = load_ids(t + kStages);
   };
   // tile 0's V^T before the loop (tile 1's loads may still fly)
   wait_vmcnt<2 * (8 / NW)>();
