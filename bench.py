@@ -604,9 +604,9 @@ def main() -> int:
     ev = {}
 
     # A step: per layer, the append of every sequence's new token and the
-    # attention. Default: gkv_decode_layer's two launches (the split, which
-    # plans, prepares the queries and appends in its prologue, then the
-    # combine); --staged: the append fused with a separate prepare launch, then
+    # attention. Default: gkv_decode_layer's launches (the split, which plans,
+    # prepares the queries and appends in its prologue, then the combine
+    # unless the split's ranges hold whole sequences); --staged: the append fused with a separate prepare launch, then
     # split and combine; --separate-append: gkv_kv_append, then the staged
     # prepare, split and combine.
     if args.separate_append:
@@ -615,6 +615,11 @@ def main() -> int:
         stages = ("append+prepare", "split", "combine")
     else:
         stages = ("append+split", "combine")
+
+    # gkv_decode_layer launches no combine where its split holds whole
+    # sequences (window layers); the step then skips it too
+    combines = [args.staged or args.separate_append or
+                gkv.layer_combines(B, Hkv, max_len, l.window, args.split_tokens) for l in layers]
 
     def step(record: bool):
         for li, layer in enumerate(layers):
@@ -626,6 +631,8 @@ def main() -> int:
                 if stage == "append":
                     gkv.kv_append(layer.qkv, Hq, cos_d, sin_d, pos_d, layer.view,
                                   seq_lens=lens_d, dev_err=err_d, stream=stream)
+                    continue
+                if stage == "combine" and not combines[li]:
                     continue
                 api = {"append+prepare": "layer_prepare",
                        "append+split": "layer_split"}.get(stage, stage)

@@ -180,7 +180,11 @@ size_t gkv_decode_workspace_bytes(int32_t B, int32_t n_kv_heads, int32_t max_seq
  *             (a multiple of 32, at most 16384)
  *   max_seq_len   host upper bound of seq_lens (sizes the grid)
  *   out       [B][out_stride] of out_dtype, heads at h*64
- * Launches gkv_decode_prepare, gkv_decode_split and gkv_decode_combine. */
+ * Two launches: a split that plans the ranges in its prologue and streams
+ * them, then the combine of the sequences that cross a range boundary. On a
+ * window layer with split_tokens 0 the ranges hold whole sequences (a range
+ * ends at most one window past its share of the stream) and the split
+ * finishes every sequence: no combine is launched. */
 int gkv_decode_attention(void *stream, int32_t B, int32_t n_q_heads, const float *q,
                          int64_t q_stride, const float *cos_tab, const float *sin_tab,
                          const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,
@@ -188,9 +192,17 @@ int gkv_decode_attention(void *stream, int32_t B, int32_t n_q_heads, const float
                          void *workspace, size_t workspace_bytes, void *out, int64_t out_stride,
                          int32_t out_dtype, uint32_t *dev_err);
 
-/* The three launches of gkv_decode_attention, for callers that time or
- * schedule them separately; same arguments, run in this order on one stream
- * with the same workspace. gkv_decode_prepare lays the sequences out as one
+/* 1 if gkv_decode_attention / gkv_decode_layer / gkv_decode_layer_noalloc
+ * launch the combine after the split for these sizes, 0 if the split
+ * finishes every sequence (window layers with split_tokens 0), < 0 on a bad
+ * argument. A caller of gkv_decode_layer_split may skip gkv_decode_combine
+ * when it returns 0 (the combine then returns at once anyway). No
+ * counterpart in the reference. */
+int gkv_decode_layer_combines(int32_t B, int32_t n_kv_heads, int32_t max_seq_len,
+                              int32_t window, int32_t split_tokens);
+
+/* The staged launches, for callers that time or schedule them separately;
+ * same arguments, run in this order on one stream with the same workspace. gkv_decode_prepare lays the sequences out as one
  * token stream cut into equal ranges (block ids checked against the pool,
  * per-step records) and prepares the rotated, scaled query operands;
  * gkv_decode_split streams every range, writes the final output of each
@@ -219,9 +231,13 @@ int gkv_decode_combine(void *stream, int32_t B, int32_t n_q_heads, int32_t n_kv_
  * ([Q | K | V] fp32, not rotated) is the new token of sequence b at position
  * seq_lens[b] - 1; its K (rotated) and V go into the cache, then the
  * attention runs as gkv_decode_attention with q = qkv, q_stride = row_stride
- * (cos_tab/sin_tab required). gkv_decode_layer_prepare is its first launch
- * (the append fused with gkv_decode_prepare); gkv_decode_split and
- * gkv_decode_combine with the same arguments (q = qkv) complete it. */
+ * (cos_tab/sin_tab required): the split launch appends the new tokens of
+ * its range in its prologue, then streams it; the combine follows unless the
+ * ranges hold whole sequences (gkv_decode_layer_combines).
+ * gkv_decode_layer_split is that first launch alone (gkv_decode_combine with
+ * the same arguments, q = qkv, completes it). gkv_decode_layer_prepare is the
+ * staged form's first launch (the append fused with gkv_decode_prepare);
+ * gkv_decode_split and gkv_decode_combine complete it. */
 int gkv_decode_layer(void *stream, int32_t B, int32_t n_q_heads, const float *qkv,
                      int64_t row_stride, const float *cos_tab, const float *sin_tab,
                      const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,

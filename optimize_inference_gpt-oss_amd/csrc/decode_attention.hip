@@ -108,6 +108,7 @@ struct DecodeArgs {
   int B;
   int n_wg;           // split workgroups launched
   int fixed_S;        // 0: S = T / n_wg (balanced); > 0: this S
+  int aligned;        // ranges of whole sequences (fused launch only; no partials)
   int32_t *plan;      // [kPlanHeader][cu: B + 1]
   int32_t *flat;      // block id of every 16-token block of the stream, per range:
                       // [range][kIdSlab], block k of range w at w * kIdSlab + k
@@ -286,6 +287,7 @@ __device__ __forceinline__ void prep_blocks(const DecodeArgs &a, int wg, int n_w
       a.plan[0] = T;
       a.plan[1] = S;
       a.plan[2] = min(a.n_wg, (T + S - 1) / S);
+      a.plan[3] = 0;
     }
   }
 
@@ -827,14 +829,47 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
       a.plan[0] = T;
       a.plan[1] = S;
       a.plan[2] = min(a.n_wg, (T + S - 1) / S);
+      a.plan[3] = a.aligned;
     }
     if (any_over && a.dev_err)
       atomicOr(a.dev_err, GKV_DEVERR_LENGTH);
   }
-  const int rs = w_id * S;
-  if (rs >= T)
-    return;
-  const int re = min(rs + S, T);
+  int rs, re;
+  if (a.aligned) {
+    // Ranges of whole sequences: range w runs from the first sequence that
+    // starts at or after w * T / n_wg to the first that starts at or after
+    // (w + 1) * T / n_wg, so every segment is a whole sequence, finished
+    // here, and no partial is written. Sequences without tokens (output 0,
+    // all weight on the sink) are written by workgroup b % n_wg.
+    auto bound = [&](int k) -> int {
+      if (k >= a.n_wg)
+        return T;
+      const int target = (int)(((int64_t)k * T + a.n_wg - 1) / a.n_wg);
+      int lo = 0, hi = B; // the first i with s_cu[i] >= target (s_cu[B] = T)
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (s_cu[mid] >= target)
+          hi = mid;
+        else
+          lo = mid + 1;
+      }
+      return s_cu[lo];
+    };
+    rs = bound(w_id);
+    re = bound(w_id + 1);
+    const int n_out = a.n_kv_heads * a.G * kHeadDim;
+    for (int b = w_id; b < B; b += a.n_wg)
+      if (s_cu[b + 1] == s_cu[b])
+        for (int i = t; i < n_out; i += nt)
+          store_out(a.out, (int64_t)b * a.out_stride + i, 0.0f, a.out_bf16);
+    if (rs >= re)
+      return;
+  } else {
+    rs = w_id * S;
+    if (rs >= T)
+      return;
+    re = min(rs + S, T);
+  }
   const int n_steps = (re - rs) / kStep;
 
   // Step records and block ids of the range. The table loads go out first;
@@ -936,6 +971,8 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
   const int lane = threadIdx.x & 63, h = lane >> 3, d0 = 8 * (lane & 7);
   if (h >= a.G)
     return;
+  if (a.plan[3])
+    return; // whole-sequence ranges: the split launch finished every sequence
   const int32_t *cu = a.plan + kPlanHeader;
   const int S = a.plan[1];
   const int c0 = cu[b], c1 = cu[b + 1];
@@ -1060,6 +1097,16 @@ static int64_t stream_max(int32_t B, int32_t max_seq_len, int32_t window) {
   return (int64_t)B * ((n_max + kStep - 1) / kStep * kStep);
 }
 
+// Window layers with the balanced split take ranges of whole sequences: no
+// sequence is split, and the fused launch needs no combine after it. A range
+// then exceeds its share of the stream by at most one sequence (W tokens), so
+// it stays within kMaxRange.
+static bool whole_sequence_ranges(int64_t t_max, int64_t n_wg, int32_t window,
+                                  int32_t split_tokens) {
+  return split_tokens == 0 && window > 0 && n_wg > 0 &&
+         (t_max + n_wg - 1) / n_wg + (window + kStep - 1) / kStep * kStep <= kMaxRange;
+}
+
 static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, int64_t q_stride,
                    const float *cos_tab, const float *sin_tab, const int32_t *seq_lens,
                    int32_t max_seq_len, const gkv_cache_view &cache, int32_t window,
@@ -1145,6 +1192,7 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
   a.B = B;
   a.n_wg = (int)n_wg;
   a.fixed_S = split_tokens;
+  a.aligned = whole_sequence_ranges(t_max, n_wg, window, split_tokens);
   char *ws = (char *)workspace;
   a.plan = (int32_t *)(ws + L.plan);
   a.flat = (int32_t *)(ws + L.flat);
@@ -1251,6 +1299,21 @@ extern "C" size_t gkv_decode_workspace_bytes(int32_t B, int32_t n_kv_heads, int3
   return layout_of(B, n_kv_heads, kMaxWorkgroups).total;
 }
 
+extern "C" int gkv_decode_layer_combines(int32_t B, int32_t n_kv_heads, int32_t max_seq_len,
+                                         int32_t window, int32_t split_tokens) {
+  if (B < 0 || n_kv_heads <= 0 || n_kv_heads > 8 || max_seq_len < 0 || window < 0 ||
+      split_tokens < 0)
+    return GKV_ERR_ARG;
+  if (B == 0)
+    return 0;
+  const int64_t t_max = stream_max(B, max_seq_len, window);
+  const int resident = resident_workgroups(n_kv_heads);
+  if (resident <= 0)
+    return GKV_ERR_HIP;
+  const int64_t n_wg = std::max<int64_t>(resident, (t_max + kMaxRange - 1) / kMaxRange);
+  return whole_sequence_ranges(t_max, n_wg, window, split_tokens) ? 0 : 1;
+}
+
 #define GKV_DECODE_PARAMS                                                                   \
   void *stream, int32_t B, int32_t n_q_heads, const float *q, int64_t q_stride,                \
       const float *cos_tab, const float *sin_tab, const int32_t *seq_lens, int32_t max_seq_len, \
@@ -1297,6 +1360,9 @@ extern "C" int gkv_decode_combine(void *stream, int32_t B, int32_t n_q_heads, in
                          workspace_bytes_, out, out_stride, out_dtype, nullptr, false);
   if (st != GKV_OK || B == 0)
     return st;
+  // always launched: after the staged launches a window layer has partials;
+  // after a fused split of whole-sequence ranges the plan says so and the
+  // kernel returns at once
   return launch_combine(a, (hipStream_t)stream);
 }
 
@@ -1307,7 +1373,7 @@ extern "C" int gkv_decode_attention(GKV_DECODE_PARAMS) {
     return st;
   if ((st = launch_fused(a, nullptr, (hipStream_t)stream)))
     return st;
-  return launch_combine(a, (hipStream_t)stream);
+  return a.aligned ? GKV_OK : launch_combine(a, (hipStream_t)stream);
 }
 
 // ---- decode layer: append + attention -----------------------------------------
@@ -1375,7 +1441,7 @@ extern "C" int gkv_decode_layer(GKV_LAYER_PARAMS) {
   GKV_LAYER_SETUP
   if ((st = launch_fused(a, &ap, (hipStream_t)stream)))
     return st;
-  return launch_combine(a, (hipStream_t)stream);
+  return a.aligned ? GKV_OK : launch_combine(a, (hipStream_t)stream);
 }
 
 
@@ -1445,5 +1511,5 @@ extern "C" int gkv_decode_layer_noalloc(void *stream, int32_t B, int32_t n_q_hea
     return st;
   if ((st = launch_fused(a, &ap, (hipStream_t)stream)))
     return st;
-  return launch_combine(a, (hipStream_t)stream);
+  return a.aligned ? GKV_OK : launch_combine(a, (hipStream_t)stream);
 }

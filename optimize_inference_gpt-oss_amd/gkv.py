@@ -87,6 +87,7 @@ SIGNATURES = {
     "gkv_qkv_append": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i32, _vp, _vp, _i32, _vp, _vp,
                                       _vp, _vp, _vp, CacheView, _vp, _i64, _vp]),
     "gkv_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32]),
+    "gkv_decode_layer_combines": (ctypes.c_int, [_i32, _i32, _i32, _i32, _i32]),
     "gkv_decode_attention": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
                                             CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64,
                                             _i32, _vp]),
@@ -253,6 +254,14 @@ def qkv_append(x, w_qkv, b_qkv, n_q_heads, cos_tab, sin_tab, view: CacheView | N
 
 def workspace_bytes(B, n_kv_heads, max_seq_len, window=0, split_tokens=0) -> int:
     return lib().gkv_decode_workspace_bytes(B, n_kv_heads, max_seq_len, window, split_tokens)
+
+
+def layer_combines(B, n_kv_heads, max_seq_len, window=0, split_tokens=0) -> bool:
+    """gkv_decode_layer_combines: whether the layer launches the combine."""
+    st = lib().gkv_decode_layer_combines(B, n_kv_heads, max_seq_len, window, split_tokens)
+    if st < 0:
+        check("gkv_decode_layer_combines", st)
+    return st == 1
 
 
 def decode_attention(q, seq_lens, max_seq_len, view: CacheView, sinks, out, window=0,

@@ -146,6 +146,16 @@ def test_decode_argument_checks(gkv):
     assert call(B=4, max_len=1 << 20, split=32, ws=fake, ws_bytes=need) == gkv.GKV_ERR_ARG
 
 
+def test_layer_combines_argument_checks(gkv):
+    L = gkv.lib()
+    assert L.gkv_decode_layer_combines(-1, 8, 100, 0, 0) == gkv.GKV_ERR_ARG
+    assert L.gkv_decode_layer_combines(4, 0, 100, 0, 0) == gkv.GKV_ERR_ARG
+    assert L.gkv_decode_layer_combines(4, 9, 100, 0, 0) == gkv.GKV_ERR_ARG
+    assert L.gkv_decode_layer_combines(4, 8, 100, -1, 0) == gkv.GKV_ERR_ARG
+    assert L.gkv_decode_layer_combines(4, 8, 100, 0, -32) == gkv.GKV_ERR_ARG
+    assert L.gkv_decode_layer_combines(0, 8, 100, 128, 0) == 0  # nothing to launch
+
+
 def test_workspace_formula(gkv):
     # plan (header + prefix sums); partial results of 2 segments per range for
     # up to 1024 ranges, 8 heads x (64 + 2) floats per kv head; then, for the

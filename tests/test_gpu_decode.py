@@ -264,3 +264,60 @@ def test_repeated_split_launches_reuse_the_plan(gkv, cuda, torch_mod):
     assert bad == 0, f"{bad} outputs out of tolerance (max err {worst:.3e})"
     for o in outs[1:]:
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+
+
+# ---- window layers: ranges of whole sequences, no combine -------------------------
+
+def test_window_layer_whole_sequence_ranges(gkv, cuda, torch_mod):
+    """A window layer with the balanced split cuts the stream only between
+    sequences (more sequences than workgroups here, lengths from 1 token to
+    past the ring), launches no combine, and matches the oracle. Each sequence
+    is then computed by one wave in a fixed order whatever the partition: with
+    some sequences emptied (length 0, output 0) the others keep their bits.
+    The staged launches on the same layer still run the combine and agree
+    within tolerance."""
+    torch = torch_mod
+    rng = np.random.default_rng(90)
+    B = 600
+    L = lens_uniform(rng, B, 0, 300)
+    L[:6] = [0, 1, 30, 126, 127, 128]
+    case = DecodeCase(B, 64, 8, L, window=128, scale=0.5, seed=91)
+    max_len = int(case.seq_lens.max())
+    assert not gkv.layer_combines(B, 8, max_len, 128, 0)
+    assert gkv.layer_combines(B, 8, max_len, 0, 0)
+    assert gkv.layer_combines(B, 8, max_len, 128, 256)
+    res = run_gpu(case, gkv, torch, cuda, layer_call=True)
+    check_case(case, res)
+
+    # the cache now holds every sequence's new token: attention only, first
+    # with the same lengths, then with some of them set to 0
+    cos, sin = gkv.rope_table(case.cos.shape[0])
+    dev = case.to_device(torch, cuda, cos, sin)
+    view = gkv.cache_view(dev["k"], dev["v"], dev["table"], case.Hkv, ring=case.ring)
+    gkv.kv_append(dev["qkv"], case.Hq, dev["cos"], dev["sin"], dev["pos"], view,
+                  seq_lens=dev["seq_lens"], dev_err=dev["err"])
+    ws = torch.empty(gkv.workspace_bytes(B, 8, max_len, 128, 0), dtype=torch.uint8, device=cuda)
+
+    def attend(lens, stages=("both",)):
+        out = torch.full((B, case.Hq * 64), float("nan"), dtype=torch.float32, device=cuda)
+        lens_d = torch.from_numpy(lens.astype(np.int32)).to(cuda)
+        for st in stages:
+            gkv.decode_attention(dev["qkv"], lens_d, max_len, view, dev["sinks"], out,
+                                 window=128, cos_tab=dev["cos"], sin_tab=dev["sin"],
+                                 workspace=ws, dev_err=dev["err"], stage=st)
+        torch.cuda.synchronize()
+        return out.cpu().numpy().reshape(B, case.Hq, 64)
+
+    full = attend(case.seq_lens)
+    assert np.array_equal(full.view(np.uint32), res["out"].view(np.uint32))
+    lens0 = case.seq_lens.copy()
+    empty = rng.choice(B, 50, replace=False)
+    lens0[empty] = 0
+    part = attend(lens0)
+    keep = np.setdiff1d(np.arange(B), empty)
+    assert np.array_equal(part[empty], np.zeros_like(part[empty]))
+    assert np.array_equal(part[keep].view(np.uint32), full[keep].view(np.uint32))
+    staged = attend(case.seq_lens, ("prepare", "split", "combine"))
+    bad, worst = allclose_report(staged, case.oracle_out())
+    assert bad == 0, f"staged: {bad} outputs out of tolerance ({worst:.3e})"
+    assert int(dev["err"].cpu().item()) == 0
