@@ -769,6 +769,7 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
   __shared__ int s_rec[kInfoSlab];
   __shared__ int s_ab[kInfoSlab]; // sequences whose new token lies in the range
   __shared__ int s_wave[kSplitWaves];
+  __shared__ int s_max[kSplitWaves];
   __shared__ int s_na;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nt = blockDim.x, B = a.B;
   const int n_waves = nt >> 6;
@@ -836,12 +837,20 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
   }
   int rs, re;
   if (a.aligned) {
-    // Ranges of whole sequences: range w runs from the first sequence that
-    // starts at or after w * T / n_wg to the first that starts at or after
-    // (w + 1) * T / n_wg, so every segment is a whole sequence, finished
-    // here, and no partial is written. Sequences without tokens (output 0,
-    // all weight on the sink) are written by workgroup b % n_wg.
-    auto bound = [&](int k) -> int {
+    // Ranges of whole sequences, so every segment is a whole sequence,
+    // finished here, and no partial is written. Two cuts, both keeping the
+    // sequences in order: by count, range k holds sequences ceil(k B / n_wg)
+    // .. ceil((k + 1) B / n_wg) - 1 (even when most sequences fill the
+    // window, where a cut by tokens can hand a range a third sequence); by
+    // tokens, range k runs from the first sequence that starts at or after
+    // k T / n_wg (even when the lengths vary below the window). The cut by
+    // count is taken when its longest range is within half a window of the
+    // mean; every workgroup finds the same. Sequences without tokens (output
+    // 0, all weight on the sink) are written by workgroup b % n_wg.
+    auto first_by_count = [&](int k) -> int {
+      return (int)(((int64_t)k * B + a.n_wg - 1) / a.n_wg);
+    };
+    auto start_by_tokens = [&](int k) -> int {
       if (k >= a.n_wg)
         return T;
       const int target = (int)(((int64_t)k * T + a.n_wg - 1) / a.n_wg);
@@ -855,8 +864,21 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
       }
       return s_cu[lo];
     };
-    rs = bound(w_id);
-    re = bound(w_id + 1);
+    int longest = 0;
+    for (int k = t; k < a.n_wg; k += nt)
+      longest = max(longest, s_cu[first_by_count(k + 1)] - s_cu[first_by_count(k)]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+      longest = max(longest, __shfl_xor(longest, off));
+    if (lane == 0)
+      s_max[wave] = longest;
+    __syncthreads();
+    for (int w = 0; w < n_waves; w++)
+      longest = max(longest, s_max[w]);
+    const bool by_count = longest <= (T + a.n_wg - 1) / a.n_wg + a.window / 2 &&
+                          longest <= kMaxRange;
+    rs = by_count ? s_cu[first_by_count(w_id)] : start_by_tokens(w_id);
+    re = by_count ? s_cu[first_by_count(w_id + 1)] : start_by_tokens(w_id + 1);
     const int n_out = a.n_kv_heads * a.G * kHeadDim;
     for (int b = w_id; b < B; b += a.n_wg)
       if (s_cu[b + 1] == s_cu[b])
