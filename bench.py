@@ -135,13 +135,16 @@ class Layer:
 def fill_cache(torch, gkv, pool, n_layers, dev, seed):
     """Random history in every cache array of the pool: bf16 N(0,1)*0.5 for K
     (and V); for an int8 V cache, random codes in [-127, 127] and scales of
-    N(0,1)*0.5 data (max |v| / 127 of 64 values, about 0.012)."""
+    N(0,1)*0.5 data (max |v| / 127 of 64 values, about 0.012); for the e4m3
+    cache, random finite codes and scales of the same data (max / 448)."""
     for layer in range(n_layers):
         v = pool.view(layer)
         n = v.num_blocks * v.n_kv_heads * 16 * D
         bases = [(v.k, "bf16"), (v.v, "int8" if v.v_format == gkv.V_INT8 else "bf16")]
         if v.v_format == gkv.V_INT8:
             bases.append((v.v_scale, "scale"))
+        if v.v_format == gkv.KV_FP8:
+            bases = [(v.k, "fp8"), (v.v, "fp8"), (v.v_scale, "scale2")]
         for i, (base, kind) in enumerate(bases):
             g = torch.Generator(device=dev)
             g.manual_seed(seed * 1000 + 3 * layer + i)
@@ -149,6 +152,15 @@ def fill_cache(torch, gkv, pool, n_layers, dev, seed):
                 t = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.5, generator=g)
             elif kind == "int8":
                 t = torch.randint(-127, 128, (n,), generator=g, device=dev, dtype=torch.int8)
+            elif kind == "fp8":
+                # random e4m3 codes without the NaN codes 0x7f, 0xff
+                t = torch.randint(0, 127, (n,), generator=g, device=dev, dtype=torch.int32)
+                t = (t | (torch.randint(0, 2, (n,), generator=g, device=dev,
+                                        dtype=torch.int32) << 7)).to(torch.uint8)
+            elif kind == "scale2":
+                # K and V scales of N(0,1)*0.5 data: max |x| / 448 of 64 values
+                t = torch.empty(2 * n // D, dtype=torch.float32, device=dev).uniform_(
+                    0.0025, 0.0045, generator=g)
             else:
                 t = torch.empty(n // D, dtype=torch.float32, device=dev).uniform_(
                     0.009, 0.015, generator=g)
@@ -171,9 +183,28 @@ def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, th
     n_blk_total = v.num_blocks
     # gather the sampled sequences' logical caches to the host
     idx = lambda kind: torch.tensor(gkv.block_offsets(kind), device="cuda").reshape(-1)  # noqa: E731
-    k_arr = gkv_cache_tensor(torch, v.k, n_blk_total, Hkv, (16, D))
-    k_arr = k_arr.view(n_blk_total, Hkv, 16 * D)[:, :, idx("k")].view(n_blk_total, Hkv, 16, D)
     v_int8 = v.v_format == gkv.V_INT8
+    kv_fp8 = v.v_format == gkv.KV_FP8
+    if kv_fp8:
+        # e4m3 codes and scales of K and V, dequantized to fp32 [block, head, token, dim]
+        # and [block, head, dim, token]
+        n = n_blk_total * Hkv * 16 * D
+        table8 = torch.from_numpy(O.fp8_table()).to("cuda")
+        kcodes = torch.empty(n, dtype=torch.uint8, device="cuda")
+        vcodes = torch.empty(n, dtype=torch.uint8, device="cuda")
+        scl = torch.empty(2 * n // D, dtype=torch.float32, device="cuda")
+        gkv.hip_memcpy_d2d(kcodes.data_ptr(), v.k, n)
+        gkv.hip_memcpy_d2d(vcodes.data_ptr(), v.v, n)
+        gkv.hip_memcpy_d2d(scl.data_ptr(), v.v_scale, 2 * n // D * 4)
+        torch.cuda.synchronize()
+        scl = scl.view(n_blk_total, Hkv, 2, 16)
+        kc8 = kcodes.view(n_blk_total, Hkv, 16 * D)[:, :, idx("k_fp8")].long()  # [token, dim]
+        k_arr = table8[kc8].view(n_blk_total, Hkv, 16, D) * scl[:, :, 0, :, None]
+        vc8 = vcodes.view(n_blk_total, Hkv, 16 * D)[:, :, idx("v_int8")].long()  # [dim, token]
+        v_arr = table8[vc8].view(n_blk_total, Hkv, D, 16) * scl[:, :, 1, None, :]
+    else:
+        k_arr = gkv_cache_tensor(torch, v.k, n_blk_total, Hkv, (16, D))
+        k_arr = k_arr.view(n_blk_total, Hkv, 16 * D)[:, :, idx("k")].view(n_blk_total, Hkv, 16, D)
     if v_int8:
         # int8 codes and scales, dequantized to fp32 [block, head, dim, token]
         n = n_blk_total * Hkv * 16 * D
@@ -185,7 +216,7 @@ def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, th
         codes = codes.view(n_blk_total, Hkv, 16 * D)[:, :, idx("v_int8")]   # [dim, token]
         v_arr = (codes.float().view(n_blk_total, Hkv, D, 16)
                  * scl.view(n_blk_total, Hkv, 1, 16))
-    else:
+    elif not kv_fp8:
         v_arr = gkv_cache_tensor(torch, v.v, n_blk_total, Hkv, (D, 16))
         v_arr = v_arr.view(n_blk_total, Hkv, 16 * D)[:, :, idx("v")].view(n_blk_total, Hkv, D, 16)
     table = table_tensor(torch, v, sample_seqs)
@@ -217,7 +248,8 @@ def cpu_baseline(torch, gkv, pool, layer_state, L, cfg, gpu_out, sample_seqs, th
             break
     dt /= reps
     n_read = np.minimum(seq_lens, W) if W else seq_lens
-    nbytes = float(n_read.sum()) * Hkv * (D * 2 + (D + 4 if v_int8 else D * 2))
+    nbytes = float(n_read.sum()) * Hkv * (2 * D + 8 if kv_fp8 else
+                                          D * 2 + (D + 4 if v_int8 else D * 2))
     got = gpu_out[:sample_seqs].float().cpu().numpy().reshape(sample_seqs, Hq, D)
     err = np.abs(got - ref)
     ok = bool(np.all(err <= 2e-3 + 1e-2 * np.abs(ref)))
@@ -513,6 +545,9 @@ def main() -> int:
     ap.add_argument("--lengths", default="random", choices=["random", "sorted", "fixed"],
                     help="diagnostics: context lengths in batch order as drawn, sorted "
                          "longest first, or all equal to the mean")
+    ap.add_argument("--kv-fp8", action="store_true",
+                    help="the e4m3 K/V cache (codes + an fp32 scale per token and head for K "
+                         "and for V; GKV_KV_FP8)")
     ap.add_argument("--v-int8", action="store_true",
                     help="the reference's int8-V cache (codes + fp32 scale per token and "
                          "head) instead of bf16 V")
@@ -570,7 +605,8 @@ def main() -> int:
     pool = gkv.Pool(n_layers=n_layers, n_kv_heads=Hkv, max_seqs=B, max_seq_len=max_len,
                     window=cfg["window"], num_blocks=need + 64,
                     shuffle_seed=0 if args.sequential_blocks else args.seed,
-                    v_format=gkv.V_INT8 if args.v_int8 else gkv.V_BF16)
+                    v_format=gkv.KV_FP8 if args.kv_fp8 else
+                    gkv.V_INT8 if args.v_int8 else gkv.V_BF16)
     seqs = [pool.seq_alloc() for _ in range(B)]
     assert seqs == list(range(B))  # row b of the batch is sequence id b
     for b in range(B):
@@ -592,8 +628,9 @@ def main() -> int:
     stream = torch.cuda.current_stream()
 
     # algorithmic bytes per cached token and kv head: K bf16 (128 B) + V bf16
-    # (128 B), or int8 V (64 B of codes + a 4-byte scale)
-    per_token = D * 2 + (D + 4 if args.v_int8 else D * 2)
+    # (128 B), or int8 V (64 B of codes + a 4-byte scale), or e4m3 K and V
+    # (64 B of codes and a 4-byte scale each)
+    per_token = 2 * D + 8 if args.kv_fp8 else D * 2 + (D + 4 if args.v_int8 else D * 2)
 
     def bytes_of(layer: Layer) -> float:
         n = np.minimum(seq_lens, layer.window) if layer.window else seq_lens
@@ -680,7 +717,7 @@ def main() -> int:
     dom_bytes = float(np.mean([bytes_of(layers[i]) for i in full]))
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
 
-    vsfx = "_int8" if args.v_int8 else ""
+    vsfx = "_fp8" if args.kv_fp8 else "_int8" if args.v_int8 else ""
     kname = "decode_fused" if stages[0] == "append+split" else "decode_split"
     traffic, traffic_note = None, "measured for the balanced split only"
     if not args.split_tokens:
@@ -718,7 +755,7 @@ def main() -> int:
             "workload": f"config {args.config}: {cfg['name']}",
             "B": B, "H_q": Hq, "H_kv": Hkv, "head_dim": D, "layers": n_layers,
             "context": f"U[{cfg['lo']},{cfg['hi']}]", "window": cfg["window"],
-            "kv_bytes_per_step": kv_bytes, "v_cache": "int8+scale" if args.v_int8 else "bf16", "split_tokens": args.split_tokens or "balanced",
+            "kv_bytes_per_step": kv_bytes, "v_cache": "fp8 K and V (e4m3) + scales" if args.kv_fp8 else "int8+scale" if args.v_int8 else "bf16", "split_tokens": args.split_tokens or "balanced",
             "pool_bytes": pool.device_bytes(),
             "kernel_ms": dict(zip(stages, (round(float(x), 4) for x in stage_ms))),
             "parallelism": "1 GPU",

@@ -73,25 +73,37 @@ typedef enum {
 
 typedef enum { GKV_F32 = 0, GKV_BF16 = 1 } gkv_dtype;
 
-/* Storage of the V cache. GKV_V_INT8 is the reference's int8-V cache
+/* Storage of the cache. GKV_V_INT8 is the reference's int8-V cache
  * (getp-csrc/kernels/fast_misc.hpp:74-84): per token and head, 64 int8 codes
- * and one fp32 scale = max|v| / 127, code = rint(v * 127 / max|v|). */
-typedef enum { GKV_V_BF16 = 0, GKV_V_INT8 = 1 } gkv_v_format;
+ * and one fp32 scale = max|v| / 127, code = rint(v * 127 / max|v|).
+ * GKV_KV_FP8 stores K and V as OCP e4m3 codes (the FP8 type of the CDNA4
+ * matrix cores: 1 sign, 4 exponent bits with bias 7, 3 mantissa bits, largest
+ * finite 448, no infinities): per token and head, 64 codes of K (after RoPE)
+ * and 64 of V, each with one fp32 scale = max|x| / 448, code = the nearest
+ * e4m3 value (ties to even) of min(max(x * (448 / max|x|), -448), 448); an
+ * all-zero head has scale 0 and codes 0. No counterpart in the reference,
+ * which names FP8 K/V as its next step after int8 V. */
+typedef enum { GKV_V_BF16 = 0, GKV_V_INT8 = 1, GKV_KV_FP8 = 2 } gkv_v_format;
 
 /* A paged cache of one layer as the kernels see it. */
 typedef struct {
-  void *k;                     /* bf16 [num_blocks][n_kv_heads][1024] (K block layout) */
+  void *k;                     /* bf16 [num_blocks][n_kv_heads][1024] (K block layout);
+                                  GKV_KV_FP8: e4m3 [num_blocks][n_kv_heads][1024], code of
+                                  token t, dim d at ((d % 32) / 8 * 16 + t) * 16 + (d / 32) * 8
+                                  + d % 8 */
   void *v;                     /* GKV_V_BF16: bf16 [num_blocks][n_kv_heads][1024] (V block
                                   layout);
-                                  GKV_V_INT8: int8 [num_blocks][n_kv_heads][1024], code of
-                                  dim d, token t at ((d % 16) * 4 + t / 4) * 16 + (d / 16) * 4
-                                  + t % 4 */
+                                  GKV_V_INT8 / GKV_KV_FP8: int8 / e4m3
+                                  [num_blocks][n_kv_heads][1024], code of dim d, token t at
+                                  ((d % 16) * 4 + t / 4) * 16 + (d / 16) * 4 + t % 4 */
   const int32_t *block_table;  /* int32 [B][table_stride] (device) */
   int32_t table_stride;        /* entries per table row */
   int32_t num_blocks;          /* physical blocks in k / v (ids are checked against it) */
   int32_t n_kv_heads;
   int32_t ring;                /* 0: slot = position; W > 0: slot = position % W */
-  void *v_scale;               /* GKV_V_INT8: fp32 [num_blocks][n_kv_heads][16]; else NULL */
+  void *v_scale;               /* GKV_V_INT8: fp32 [num_blocks][n_kv_heads][16] (V scale of
+                                  token t at t); GKV_KV_FP8: fp32 [num_blocks][n_kv_heads][32]
+                                  (K scale of token t at t, V scale at 16 + t); else NULL */
   int32_t v_format;            /* gkv_v_format (0: bf16) */
 } gkv_cache_view;
 

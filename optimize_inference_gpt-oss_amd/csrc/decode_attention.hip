@@ -99,7 +99,8 @@ struct DecodeArgs {
   const float *cos_tab, *sin_tab;
   const int32_t *seq_lens;
   const uint16_t *kc, *vc;
-  const float *vs;    // int8 V: fp32 scales [block][head][16]
+  const float *vs;    // int8 V: fp32 scales [block][head][16]; e4m3 K/V: [block][head][32]
+  int kv_fp8;         // K and V as e4m3 codes + scales (GKV_KV_FP8)
   const int32_t *table;
   int table_stride, num_blocks, n_kv_heads, window;
   int max_len;        // host bound of the tokens attended per sequence
@@ -162,6 +163,15 @@ __device__ __forceinline__ u32x2 int8x4_to_bf16x4(uint32_t w) {
     h[i] = __float_as_uint((float)c) >> 16;
   }
   return u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+}
+
+// Four e4m3 codes (one per byte) -> four bf16 (exact: every e4m3 value is a
+// bf16 value), in order.
+__device__ __forceinline__ u32x2 fp8x4_to_bf16x4(uint32_t w) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+  return u32x2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
 }
 
 // ---- prep -----------------------------------------------------------------------
@@ -374,10 +384,14 @@ __global__ __launch_bounds__(kPrepThreads) void decode_layer_prep_kernel(DecodeA
 // sequences' lengths, in LDS), rotated, scaled and split into the operand
 // pieces when the segment opens; otherwise the ring carries the operand
 // pieces prepared by the prepare launch (a.qops).
-template <int R, bool VQ, bool RAWQ>
+// VF: the cache's value format, 0 bf16 K/V, 1 int8 V (+ scales), 2 e4m3 K and
+// V (+ scales).
+template <int R, int VF, bool RAWQ>
 __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, const int2 *s_ids,
                                              const int *s_rec, const int *s_len, int n_steps) {
   constexpr int D = kHeadDim;
+  constexpr bool VQ = VF != 0;  // V as codes with a scale per token
+  constexpr bool KF8 = VF == 2; // K as e4m3 codes with a scale per token
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); // wave-uniform
   const int n_waves = blockDim.x >> 6;
@@ -426,6 +440,27 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
     bb = (p0 == kBadBlock ? 1 : 0) | (p1 == kBadBlock ? 2 : 0) | (pass << 2);
     p0 = max(p0, 0);
     p1 = max(p1, 0);
+    if (KF8) {
+      // e4m3 K and V: per block one 16-byte piece of K codes (dims 8kg ..
+      // +7 and 32+8kg .. +7 of token col), one of V codes (as int8 V), and
+      // the 4 scales of tokens 4kg .. 4kg+3 for K and for V
+      const size_t c0 = ((size_t)p0 * a.n_kv_heads + g) * (head_bytes / 2);
+      const size_t c1 = ((size_t)p1 * a.n_kv_heads + g) * (head_bytes / 2);
+      const __amdgpu_buffer_rsrc_t k0 = head_rsrc((const char *)a.kc + c0);
+      const __amdgpu_buffer_rsrc_t k1 = head_rsrc((const char *)a.kc + c1);
+      const __amdgpu_buffer_rsrc_t v0 = head_rsrc((const char *)a.vc + c0);
+      const __amdgpu_buffer_rsrc_t v1 = head_rsrc((const char *)a.vc + c1);
+      const __amdgpu_buffer_rsrc_t s0 = head_rsrc((const char *)a.vs + c0 / 8);
+      const __amdgpu_buffer_rsrc_t s1 = head_rsrc((const char *)a.vs + c1 / 8);
+      kr[0] = __builtin_amdgcn_raw_buffer_load_b128(k0, kv_off, 0, kKvAux);
+      kr[1] = __builtin_amdgcn_raw_buffer_load_b128(k1, kv_off, 0, kKvAux);
+      kr[2] = __builtin_amdgcn_raw_buffer_load_b128(s0, 16 * kg, 0, kKvAux);
+      kr[3] = __builtin_amdgcn_raw_buffer_load_b128(s1, 16 * kg, 0, kKvAux);
+      vr[0] = __builtin_amdgcn_raw_buffer_load_b128(v0, vq_off, 0, kKvAux);
+      vr[1] = __builtin_amdgcn_raw_buffer_load_b128(v1, vq_off, 0, kKvAux);
+      vr[2] = __builtin_amdgcn_raw_buffer_load_b128(s0, 64 + 16 * kg, 0, kKvAux);
+      vr[3] = __builtin_amdgcn_raw_buffer_load_b128(s1, 64 + 16 * kg, 0, kKvAux);
+    } else {
     const size_t h0 = ((size_t)p0 * a.n_kv_heads + g) * head_bytes;
     const size_t h1 = ((size_t)p1 * a.n_kv_heads + g) * head_bytes;
     const __amdgpu_buffer_rsrc_t k0 = head_rsrc((const char *)a.kc + h0);
@@ -459,6 +494,7 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
         vr[2 * h] = u32x4{x[0], x[1], y[0], y[1]};
         vr[2 * h + 1] = u32x4{x[2], x[3], y[2], y[3]};
       }
+    }
     }
     if ((rc & 0x80) || step == 0) { // the step opens a segment: its query
       const int b = rc >> 8;
@@ -617,14 +653,26 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
     float sc[8];
 #pragma unroll
     for (int jt = 0; jt < 2; jt++) {
+      bf16x8 k0, k1;
+      if (KF8) {
+        // the codes in bf16 (exact); the token's scale multiplies its score
+        const u32x2 c0 = fp8x4_to_bf16x4(kr[jt][0]), c1 = fp8x4_to_bf16x4(kr[jt][1]);
+        const u32x2 c2 = fp8x4_to_bf16x4(kr[jt][2]), c3 = fp8x4_to_bf16x4(kr[jt][3]);
+        k0 = __builtin_bit_cast(bf16x8, u32x4{c0[0], c0[1], c1[0], c1[1]});
+        k1 = __builtin_bit_cast(bf16x8, u32x4{c2[0], c2[1], c3[0], c3[1]});
+      } else {
+        k0 = __builtin_bit_cast(bf16x8, kr[2 * jt + 0]);
+        k1 = __builtin_bit_cast(bf16x8, kr[2 * jt + 1]);
+      }
       f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * jt + 0]),
-                                                    qop0, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[2 * jt + 1]),
-                                                    qop1, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qop0, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qop1, acc, 0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < 4; r++)
+      for (int r = 0; r < 4; r++) {
         sc[4 * jt + r] = acc[r] + swap8(acc[r]);
+        if (KF8)
+          sc[4 * jt + r] *= __uint_as_float(kr[2 + jt][r]);
+      }
     }
     if (valid < kStep || bad) {
       // Tail of the sequence, padding, past the range, or a bad block id:
@@ -637,6 +685,16 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
         for (int r = 0; r < 4; r++)
           if (16 * jt + 4 * kg + r >= valid || blk_bad)
             sc[4 * jt + r] = -INFINITY;
+        if (KF8) {
+          // e4m3 codes of unwritten slots may be NaN: zero them
+          uint32_t keep = 0;
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            keep |= (16 * jt + 4 * kg + r < valid && !blk_bad) ? 0xffu << (8 * r) : 0u;
+#pragma unroll
+          for (int nn = 0; nn < 4; nn++)
+            vr[jt][nn] &= keep;
+        }
 #pragma unroll
         for (int h2 = 0; h2 < 2 && !VQ; h2++) {
           const int tk = 16 * jt + 4 * kg + 2 * h2;
@@ -677,8 +735,8 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
       lsum += p[i];
     }
     if (VQ) {
-      // int8 V: the token's scale goes into its weight (the codes are exact
-      // in bf16); a masked token's weight is 0 whatever its scale holds
+      // int8 / e4m3 V: the token's scale goes into its weight (the codes are
+      // exact in bf16); a masked token's weight is 0 whatever its scale holds
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         const float sc_t = __uint_as_float(vr[2 + (i >> 2)][i & 3]);
@@ -687,7 +745,8 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
       const bf16x8 pop = pack_pieces(p, lo);
 #pragma unroll
       for (int nn = 0; nn < 4; nn++) {
-        const u32x2 x = int8x4_to_bf16x4(vr[0][nn]), y = int8x4_to_bf16x4(vr[1][nn]);
+        const u32x2 x = KF8 ? fp8x4_to_bf16x4(vr[0][nn]) : int8x4_to_bf16x4(vr[0][nn]);
+        const u32x2 y = KF8 ? fp8x4_to_bf16x4(vr[1][nn]) : int8x4_to_bf16x4(vr[1][nn]);
         const bf16x8 vop = __builtin_bit_cast(bf16x8, u32x4{x[0], x[1], y[0], y[1]});
         o[nn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop, o[nn], 0, 0, 0);
       }
@@ -718,7 +777,7 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
 
 // The split launch of the staged path: the plan, block ids and step records
 // come from the prepare launch through the workspace.
-template <int R, bool VQ>
+template <int R, int VF>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(1)))
 void decode_split_kernel(DecodeArgs a) {
   const int w_id = blockIdx.x;
@@ -743,7 +802,7 @@ void decode_split_kernel(DecodeArgs a) {
   if (rs >= T)
     return;
   const int re = min(rs + S, T);
-  stream_range<R, VQ, false>(a, w_id, s_ids, s_rec, nullptr, (re - rs) / kStep);
+  stream_range<R, VF, false>(a, w_id, s_ids, s_rec, nullptr, (re - rs) / kStep);
 }
 
 // ---- fused: plan, append and split in one launch --------------------------------
@@ -760,7 +819,7 @@ constexpr int kStepsPerThread = kInfoSlab / 64; // record-building steps per thr
 // reads the new tokens back; no other workgroup reads them (each step of the
 // stream belongs to one range). Workgroup 0 publishes the plan for the
 // combine.
-template <int R, bool VQ>
+template <int R, int VF>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(1)))
 void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
   __shared__ int s_cu[kMaxBatch + 1];
@@ -976,7 +1035,7 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
   KernargPtr pa = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
   asm volatile("" : "+s"(pa));
   const DecodeArgs a2 = *pa;
-  stream_range<R, VQ, true>(a2, w_id, s_ids, s_rec, s_len, n_steps);
+  stream_range<R, VF, true>(a2, w_id, s_ids, s_rec, s_len, n_steps);
 #endif
 }
 
@@ -1052,21 +1111,23 @@ static int ring_depth() {
 
 template <int R>
 static void launch_split_ring(const DecodeArgs &a, dim3 grid, dim3 block, hipStream_t s) {
-  if (a.vs)
-    hipLaunchKernelGGL((decode_split_kernel<R, true>), grid, block, 0, s, a);
+  if (a.kv_fp8)
+    hipLaunchKernelGGL((decode_split_kernel<R, 2>), grid, block, 0, s, a);
+  else if (a.vs)
+    hipLaunchKernelGGL((decode_split_kernel<R, 1>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL((decode_split_kernel<R, false>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((decode_split_kernel<R, 0>), grid, block, 0, s, a);
 }
 
 // The fused kernel at the given ring depth (3..5; the default otherwise).
 static const void *fused_kernel_fn(int ring) {
   switch (ring) {
   case 3:
-    return (const void *)decode_fused_kernel<3, false>;
+    return (const void *)decode_fused_kernel<3, 0>;
   case 5:
-    return (const void *)decode_fused_kernel<5, false>;
+    return (const void *)decode_fused_kernel<5, 0>;
   default:
-    return (const void *)decode_fused_kernel<4, false>;
+    return (const void *)decode_fused_kernel<4, 0>;
   }
 }
 
@@ -1144,9 +1205,10 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
     return GKV_ERR_ARG;
   if (n_q_heads % cache.n_kv_heads != 0)
     return GKV_ERR_ARG;
-  if (cache.v_format != GKV_V_BF16 && cache.v_format != GKV_V_INT8)
+  if (cache.v_format != GKV_V_BF16 && cache.v_format != GKV_V_INT8 &&
+      cache.v_format != GKV_KV_FP8)
     return GKV_ERR_ARG;
-  if (need_cache && cache.v_format == GKV_V_INT8 && !cache.v_scale)
+  if (need_cache && cache.v_format != GKV_V_BF16 && !cache.v_scale)
     return GKV_ERR_ARG;
   if (cache.n_kv_heads > 8 || B > kMaxBatch)
     return GKV_ERR_UNSUPPORTED; // combine: one wave per kv head; prep: prefix sums in LDS
@@ -1202,7 +1264,8 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
   a.seq_lens = seq_lens;
   a.kc = (const uint16_t *)cache.k;
   a.vc = (const uint16_t *)cache.v;
-  a.vs = cache.v_format == GKV_V_INT8 ? (const float *)cache.v_scale : nullptr;
+  a.vs = cache.v_format != GKV_V_BF16 ? (const float *)cache.v_scale : nullptr;
+  a.kv_fp8 = cache.v_format == GKV_KV_FP8;
   a.table = cache.block_table;
   a.table_stride = cache.table_stride;
   a.num_blocks = cache.num_blocks;
@@ -1276,10 +1339,12 @@ static int launch_split(const DecodeArgs &a, hipStream_t s) {
 template <int R>
 static void launch_fused_ring(const DecodeArgs &a, const AppendArgs &ap, int append, dim3 grid,
                               dim3 block, hipStream_t s) {
-  if (a.vs)
-    hipLaunchKernelGGL((decode_fused_kernel<R, true>), grid, block, 0, s, a, ap, append);
+  if (a.kv_fp8)
+    hipLaunchKernelGGL((decode_fused_kernel<R, 2>), grid, block, 0, s, a, ap, append);
+  else if (a.vs)
+    hipLaunchKernelGGL((decode_fused_kernel<R, 1>), grid, block, 0, s, a, ap, append);
   else
-    hipLaunchKernelGGL((decode_fused_kernel<R, false>), grid, block, 0, s, a, ap, append);
+    hipLaunchKernelGGL((decode_fused_kernel<R, 0>), grid, block, 0, s, a, ap, append);
 }
 
 // The fused launch; ap == nullptr: no append (attention only).
@@ -1432,6 +1497,7 @@ static int layer_append_args(AppendArgs &ap, int32_t B, int32_t n_q_heads, const
   ap.k_pack = ap.v_pack = nullptr;
   ap.dev_err = dev_err;
   ap.v_int8 = cache.v_format == GKV_V_INT8;
+  ap.kv_fp8 = cache.v_format == GKV_KV_FP8;
   ap.vs = (float *)cache.v_scale;
   (void)B;
   return GKV_OK;

@@ -36,7 +36,7 @@ __global__ __launch_bounds__(64 * kRowsPerWg) void kv_append_kernel(AppendArgs a
   __shared__ int64_t s_base[kRowsPerWg];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r = blockIdx.x * kRowsPerWg + w;
-  const bool staged = !a.v_int8 && a.vc && a.n_kv_heads <= kMaxStageHeads;
+  const bool staged = !a.v_int8 && !a.kv_fp8 && a.vc && a.n_kv_heads <= kMaxStageHeads;
   RowPlace pl{0, -1, -1, 0};
   if (r < n_rows)
     pl = append_row(a, r, lane, 0, 1, staged ? s_v[w] : nullptr);
@@ -109,9 +109,10 @@ extern "C" int gkv_kv_append(void *stream, int32_t n_rows, const float *qkv, int
     return GKV_ERR_ARG;
   if (cache.ring % kBlockTokens != 0)
     return GKV_ERR_UNSUPPORTED;
-  if (cache.v_format != GKV_V_BF16 && cache.v_format != GKV_V_INT8)
+  if (cache.v_format != GKV_V_BF16 && cache.v_format != GKV_V_INT8 &&
+      cache.v_format != GKV_KV_FP8)
     return GKV_ERR_ARG;
-  if (to_cache && cache.v_format == GKV_V_INT8 && !cache.v_scale)
+  if (to_cache && cache.v_format != GKV_V_BF16 && !cache.v_scale)
     return GKV_ERR_ARG;
   // On a ring, two rows of one sequence W positions apart take the same slot;
   // only the lengths tell which of them the ring keeps.
@@ -141,6 +142,7 @@ extern "C" int gkv_kv_append(void *stream, int32_t n_rows, const float *qkv, int
   a.v_pack = (uint16_t *)v_pack;
   a.dev_err = dev_err;
   a.v_int8 = cache.v_format == GKV_V_INT8;
+  a.kv_fp8 = cache.v_format == GKV_KV_FP8;
   a.vs = (float *)cache.v_scale;
   hipLaunchKernelGGL(kv_append_kernel, dim3((n_rows + kRowsPerWg - 1) / kRowsPerWg),
                      dim3(64 * kRowsPerWg), 0, (hipStream_t)stream, a, n_rows);

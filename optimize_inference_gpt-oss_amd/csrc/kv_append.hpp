@@ -19,8 +19,9 @@ struct AppendArgs {
   int64_t q_out_stride;
   uint16_t *k_pack, *v_pack;
   uint32_t *dev_err;
-  float *vs;   // int8 V: fp32 scales [block][head][16]; nullptr for bf16 V
+  float *vs;   // int8 V: fp32 scales [block][head][16]; fp8 K/V: [block][head][32]
   int v_int8;  // 1: V is stored as int8 codes + scales (gkv_v_format GKV_V_INT8)
+  int kv_fp8;  // 1: K and V are stored as e4m3 codes + scales (GKV_KV_FP8)
 };
 
 // Element offset of token t, dim d inside one head's bf16 K block (16 x 64
@@ -43,6 +44,23 @@ __host__ __device__ __forceinline__ int v_offset(int t, int d) {
 // tokens 4kg..4kg+3 in one 16-byte piece.
 __host__ __device__ __forceinline__ int v_int8_offset(int d, int t) {
   return ((d % 16) * 4 + t / 4) * 16 + (d / 16) * 4 + t % 4;
+}
+
+// Offset of token t, dim d inside one head's 1 KB e4m3 K block: lane kg * 16
+// + t of the attention kernel finds dims 8kg .. 8kg+7 and 32+8kg .. +7 of
+// token t (its two matrix-op pieces) in one 16-byte piece, in lane order.
+__host__ __device__ __forceinline__ int k_fp8_offset(int t, int d) {
+  return ((d % 32) / 8 * 16 + t) * 16 + (d / 32) * 8 + d % 8;
+}
+
+// The e4m3 codes of x * inv, clamped to the largest finite value 448
+// (the conversion rounds to nearest even and does not saturate), four values
+// per dword, element 0 in the low byte.
+__device__ __forceinline__ uint32_t fp8x4(float x0, float x1, float x2, float x3, float inv) {
+  auto c = [inv](float x) { return fminf(fmaxf(x * inv, -448.0f), 448.0f); };
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(c(x0), c(x1), 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c(x2), c(x3), w, true);
+  return (uint32_t)w;
 }
 
 // Eight bf16 (bits) as one 16-byte piece, element 0 first.
@@ -132,16 +150,35 @@ __device__ __forceinline__ RowPlace append_row(const AppendArgs &a, int r, int l
       const f32x4 *cp = (const f32x4 *)(cs + 8 * j), *sp = (const f32x4 *)(sn + 8 * j);
       const f32x4 x1[2] = {k1p[0], k1p[1]}, x2[2] = {k2p[0], k2p[1]};
       const f32x4 c[2] = {cp[0], cp[1]}, s[2] = {sp[0], sp[1]};
+      float f1[8], f2[8];
       uint16_t o1[8], o2[8];
 #pragma unroll
       for (int i = 0; i < 8; i++) {
         const float a1 = x1[i / 4][i % 4], a2 = x2[i / 4][i % 4];
         const float cc = c[i / 4][i % 4], ss = s[i / 4][i % 4];
-        o1[i] = f32_to_bf16_rne(rope_first(a1, a2, cc, ss));
-        o2[i] = f32_to_bf16_rne(rope_second(a1, a2, cc, ss));
+        f1[i] = rope_first(a1, a2, cc, ss);
+        f2[i] = rope_second(a1, a2, cc, ss);
+        o1[i] = f32_to_bf16_rne(f1[i]);
+        o2[i] = f32_to_bf16_rne(f2[i]);
       }
       const u32x4 p1 = pack8(o1), p2 = pack8(o2);
-      if (store) {
+      if (store && a.kv_fp8) {
+        // e4m3 K: the head's max |k| over its 4 lanes, then one scale per
+        // token and head; the lane's 16 codes are one 16-byte piece
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+          amax = fmaxf(amax, fmaxf(fabsf(f1[i]), fabsf(f2[i])));
+        amax = fmaxf(amax, __shfl_xor(amax, 1));
+        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+        const u32x4 w{fp8x4(f1[0], f1[1], f1[2], f1[3], inv), fp8x4(f1[4], f1[5], f1[6], f1[7], inv),
+                      fp8x4(f2[0], f2[1], f2[2], f2[3], inv), fp8x4(f2[4], f2[5], f2[6], f2[7], inv)};
+        const int64_t hb = kbase + (int64_t)g * (kBlockTokens * D); // bytes: 1 KB per head
+        *(u32x4 *)((uint8_t *)a.kc + hb + k_fp8_offset(off, 8 * j)) = w;
+        if (j == 0)
+          a.vs[hb / 32 + off] = amax / 448.0f;
+      } else if (store) {
         uint16_t *kd = a.kc + kbase + (int64_t)g * (kBlockTokens * D);
         *(u32x4 *)(kd + k_offset(off, 8 * j)) = p1;
         *(u32x4 *)(kd + k_offset(off, HALF + 8 * j)) = p2;
@@ -167,14 +204,35 @@ __device__ __forceinline__ RowPlace append_row(const AppendArgs &a, int r, int l
       *(u32x4 *)vpk = pack8(h);
       *(u32x4 *)(vpk + 8) = pack8(h + 8);
     }
-    if (v_stage && !a.v_int8) {
+    if (v_stage && !a.v_int8 && !a.kv_fp8) {
       *(u32x4 *)(v_stage + g * D + 16 * q) = pack8(h);
       *(u32x4 *)(v_stage + g * D + 16 * q + 8) = pack8(h + 8);
       continue;
     }
     if (!store)
       continue;
-    if (a.v_int8) {
+    if (a.kv_fp8) {
+      // e4m3 V: the head's max |v| over its 4 lanes, one scale per token and
+      // head (after the token's K scale), codes in the int8 V layout
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; i++)
+        amax = fmaxf(amax, fabsf(x[i / 4][i % 4]));
+      amax = fmaxf(amax, __shfl_xor(amax, 1));
+      amax = fmaxf(amax, __shfl_xor(amax, 2));
+      const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+      const int64_t hb = vbase + (int64_t)g * (kBlockTokens * D); // bytes: 1 KB per head
+      uint8_t *vq = (uint8_t *)a.vc + hb;
+#pragma unroll
+      for (int i = 0; i < 16; i += 4) {
+        const uint32_t w = fp8x4(x[i / 4][0], x[i / 4][1], x[i / 4][2], x[i / 4][3], inv);
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+          vq[v_int8_offset(16 * q + i + k, off)] = (uint8_t)(w >> (8 * k));
+      }
+      if (q == 0)
+        a.vs[hb / 32 + kBlockTokens + off] = amax / 448.0f;
+    } else if (a.v_int8) {
       // The head's max |v| over its 4 lanes, then the reference's rule,
       // getp-csrc/kernels/fast_misc.hpp:74-84.
       float amax = 0.0f;

@@ -64,16 +64,21 @@ struct gkv_pool {
   }
 };
 
-// Bytes of one 16-token block of one layer: K bf16, V bf16 or int8 + fp32 scales.
-static int64_t k_bytes(int n_kv_heads) { return (int64_t)n_kv_heads * kBT * kD * 2; }
+// Bytes of one 16-token block of one layer: K bf16 (or e4m3), V bf16 (or int8
+// or e4m3 codes) + fp32 scales (V's, or K's and V's).
+static int64_t k_bytes(int n_kv_heads, int v_format) {
+  return (int64_t)n_kv_heads * kBT * kD * (v_format == GKV_KV_FP8 ? 1 : 2);
+}
 static int64_t v_bytes(int n_kv_heads, int v_format) {
-  return v_format == GKV_V_INT8 ? (int64_t)n_kv_heads * kBT * kD : k_bytes(n_kv_heads);
+  return (int64_t)n_kv_heads * kBT * kD * (v_format == GKV_V_BF16 ? 2 : 1);
 }
 static int64_t s_bytes(int n_kv_heads, int v_format) {
-  return v_format == GKV_V_INT8 ? (int64_t)n_kv_heads * kBT * 4 : 0;
+  return (int64_t)n_kv_heads * kBT * 4 *
+         (v_format == GKV_V_INT8 ? 1 : v_format == GKV_KV_FP8 ? 2 : 0);
 }
 static int64_t block_bytes_per_layer(int n_kv_heads, int v_format) {
-  return k_bytes(n_kv_heads) + v_bytes(n_kv_heads, v_format) + s_bytes(n_kv_heads, v_format);
+  return k_bytes(n_kv_heads, v_format) + v_bytes(n_kv_heads, v_format) +
+         s_bytes(n_kv_heads, v_format);
 }
 
 extern "C" int gkv_pool_create(const gkv_pool_config *cfg, gkv_pool **out) {
@@ -86,7 +91,7 @@ extern "C" int gkv_pool_create(const gkv_pool_config *cfg, gkv_pool **out) {
     return GKV_ERR_ARG;
   if (c.head_dim != kD || c.window % kBT != 0)
     return GKV_ERR_UNSUPPORTED;
-  if (c.v_format != GKV_V_BF16 && c.v_format != GKV_V_INT8)
+  if (c.v_format != GKV_V_BF16 && c.v_format != GKV_V_INT8 && c.v_format != GKV_KV_FP8)
     return GKV_ERR_ARG;
   gkv_pool *p = new (std::nothrow) gkv_pool();
   if (!p)
@@ -143,7 +148,7 @@ extern "C" int gkv_pool_create(const gkv_pool_config *cfg, gkv_pool **out) {
     p->device_bytes += bytes;
     return true;
   };
-  const int64_t kb = k_bytes(c.n_kv_heads), vb = v_bytes(c.n_kv_heads, c.v_format);
+  const int64_t kb = k_bytes(c.n_kv_heads, c.v_format), vb = v_bytes(c.n_kv_heads, c.v_format);
   const int64_t sb = s_bytes(c.n_kv_heads, c.v_format);
   bool ok = true;
   p->k_full.assign(p->n_full, nullptr);

@@ -356,6 +356,8 @@ extern "C" int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64
     return GKV_ERR_ARG; // rows W positions apart share a ring slot: the lengths pick the kept one
   if (cache.ring % kBlockTokens != 0)
     return GKV_ERR_UNSUPPORTED;
+  if (cache.v_format == GKV_KV_FP8)
+    return GKV_ERR_UNSUPPORTED; // the epilogue stores bf16 K (gkv_kv_append stores e4m3)
   if (cache.v_format != GKV_V_BF16 && cache.v_format != GKV_V_INT8)
     return GKV_ERR_ARG;
   if (to_cache && cache.v_format == GKV_V_INT8 && !cache.v_scale)
@@ -402,6 +404,7 @@ extern "C" int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64
   ap.v_pack = nullptr;
   ap.dev_err = dev_err;
   ap.v_int8 = cache.v_format == GKV_V_INT8;
+  ap.kv_fp8 = 0;
   ap.vs = (float *)cache.v_scale;
   if (big)
     hipLaunchKernelGGL(

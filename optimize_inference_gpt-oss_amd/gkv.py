@@ -41,7 +41,7 @@ class CacheView(ctypes.Structure):
                 ("v_scale", _vp), ("v_format", _i32)]
 
 
-V_BF16, V_INT8 = 0, 1
+V_BF16, V_INT8, KV_FP8 = 0, 1, 2
 
 
 def block_offsets(kind: str):
@@ -49,7 +49,11 @@ def block_offsets(kind: str):
     csrc/kv_append.hpp lay it out), as nested lists:
     - "k": [16 tokens][64 dims] of the bf16 K block (2 KB),
     - "v": [64 dims][16 tokens] of the bf16 V block (2 KB),
-    - "v_int8": [64 dims][16 tokens] of the int8 V block (1 KB)."""
+    - "v_int8": [64 dims][16 tokens] of the int8 V block (1 KB), also the e4m3 V block,
+    - "k_fp8": [16 tokens][64 dims] of the e4m3 K block (1 KB)."""
+    if kind == "k_fp8":
+        return [[((d % 32) // 8 * 16 + t) * 16 + (d // 32) * 8 + d % 8 for d in range(64)]
+                for t in range(16)]
     if kind == "k":
         return [[(d // 32) * 512 + ((d % 32) // 8 * 16 + t) * 8 + d % 8 for d in range(64)]
                 for t in range(16)]
@@ -217,13 +221,16 @@ def rope_table(n_pos: int, **overrides):
     return c, s
 
 
-def cache_view(k, v, block_table, n_kv_heads: int, ring: int = 0, v_scale=None) -> CacheView:
+def cache_view(k, v, block_table, n_kv_heads: int, ring: int = 0, v_scale=None,
+               v_format=None) -> CacheView:
     """View over torch tensors k [NB, Hkv, 16, 64], v [NB, Hkv, 64, 16] (bf16 or int16),
     block_table int32 [B, stride]. With v_scale (fp32 [NB, Hkv, 16]) the V cache is
-    int8 codes [NB, Hkv, 1024] (GKV_V_INT8)."""
+    int8 codes [NB, Hkv, 1024] (GKV_V_INT8); v_format=KV_FP8: k and v are e4m3 codes
+    [NB, Hkv, 1024] and v_scale fp32 [NB, Hkv, 32] (K scales, then V scales)."""
+    if v_format is None:
+        v_format = V_INT8 if v_scale is not None else V_BF16
     return CacheView(ptr(k), ptr(v), ptr(block_table), int(block_table.shape[1]),
-                     int(k.shape[0]), int(n_kv_heads), int(ring), ptr(v_scale),
-                     V_INT8 if v_scale is not None else V_BF16)
+                     int(k.shape[0]), int(n_kv_heads), int(ring), ptr(v_scale), int(v_format))
 
 
 def kv_append(qkv, n_q_heads, cos_tab, sin_tab, row_pos, view: CacheView, row_seq=None,

@@ -31,6 +31,12 @@
  *       (getp-csrc/tests/attn_test.cpp, built into oracle/_ref/libref_q8.so)
  *       on random heads; closed forms: exact multiples of the step, the amax
  *       element at +-127, ties to even, the all-zero head.
+ *   orc_fp8_value, orc_quantize_fp8  (the e4m3 K/V cache, which the
+ *       reference does not implement: it names FP8 K/V as its next step)
+ *       pinned by the format's closed forms (1.0 = 0x38, 448 = 0x7e, 2^-6 =
+ *       0x08, 2^-9 = 0x01, 0x7f NaN, monotone codes, sign symmetry) and by
+ *       brute force: every code equals the nearest table value, ties to the
+ *       even code, over random values, all midpoints and the edges.
  */
 #include "kv_oracle.h"
 
@@ -319,5 +325,50 @@ void orc_linear(int n_rows, const float *x, long x_stride, const float *w, const
     if (bias)
       o += bias[i];
     out[r * out_stride + i] = o;
+  }
+}
+
+/* ---- e4m3 (OCP FP8 E4M3) K/V cache ----------------------------------------
+ * Not in the reference (its next step after int8 V). Format: sign, 4 exponent
+ * bits (bias 7), 3 mantissa bits; exponent 0 holds the subnormals m * 2^-9;
+ * S.1111.111 is NaN; no infinities; largest finite 448. */
+float orc_fp8_value(uint8_t c) {
+  const int e = (c >> 3) & 15, m = c & 7;
+  if (e == 15 && m == 7)
+    return NAN;
+  const float v = e == 0 ? ldexpf((float)m, -9) : ldexpf((float)(8 + m), e - 10);
+  return (c & 0x80) ? -v : v;
+}
+
+/* The e4m3 code nearest to x (|x| <= 448), ties to the even code. */
+static uint8_t fp8_code(float x) {
+  uint32_t b;
+  memcpy(&b, &x, 4);
+  const uint8_t s = (uint8_t)((b >> 24) & 0x80u);
+  const float a = fabsf(x);
+  if (a < 0x1p-6f) /* subnormal steps of 2^-9; 8 steps is code 0x08 = 2^-6 */
+    return s | (uint8_t)rintf(a * 0x1p9f);
+  uint32_t ab = b & 0x7fffffffu;
+  ab += 0x7ffffu + ((ab >> 20) & 1u); /* 23 mantissa bits -> 3, ties to even */
+  const int e = (int)(ab >> 23) - 127 + 7;
+  return s | (uint8_t)((e << 3) | ((ab >> 20) & 7u));
+}
+
+/* Per head of head_dim values: amax, the reciprocal 448/amax rounded once,
+ * each value times it, clamped to +-448 and rounded to the nearest e4m3 code
+ * (ties to even); scale = amax / 448. An all-zero head: scale 0, codes 0. */
+void orc_quantize_fp8(const float *x, int n_heads, int head_dim, uint8_t *codes,
+                      float *scales) {
+  for (int h = 0; h < n_heads; h++) {
+    const float *xh = x + (long)h * head_dim;
+    float amax = 0.0f;
+    for (int i = 0; i < head_dim; i++)
+      amax = fmaxf(amax, fabsf(xh[i]));
+    const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+    for (int i = 0; i < head_dim; i++) {
+      const float c = fminf(fmaxf(xh[i] * inv, -448.0f), 448.0f);
+      codes[(long)h * head_dim + i] = fp8_code(c);
+    }
+    scales[h] = amax / 448.0f;
   }
 }

@@ -102,6 +102,11 @@ void orc_kv_append(int B, int n_q_heads, int n_kv_heads, int head_dim, const flo
  * getp-csrc/tests/attn_test.cpp:218-226 (quantize_v).
  *   v[h*head_dim + i] fp32 -> codes[h*head_dim + i], scales[h] */
 void orc_quantize_v(const float *v, int n_heads, int head_dim, int8_t *codes, float *scales);
+/* e4m3 (OCP FP8 E4M3) cache: the value of a code, and per-head quantization
+ * (scale = amax / 448, code = nearest e4m3 of clamp(x * 448 / amax)). */
+float orc_fp8_value(uint8_t c);
+void orc_quantize_fp8(const float *x, int n_heads, int head_dim, uint8_t *codes,
+                      float *scales);
 
 #ifdef __cplusplus
 }

@@ -61,6 +61,9 @@ def lib():
                                             _vp, _l, _i]
         L.orc_prefill_attention.restype = _i
         L.orc_quantize_v.argtypes = [_vp, _i, _i, _vp, _vp]
+        L.orc_quantize_fp8.argtypes = [_vp, _i, _i, _vp, _vp]
+        L.orc_fp8_value.argtypes = [ctypes.c_uint8]
+        L.orc_fp8_value.restype = ctypes.c_float
         L.orc_linear.argtypes = [_i, _vp, _l, _vp, _vp, _i, _i, _vp, _l]
         L.orc_kv_append.argtypes = [_i, _i, _i, _i, _vp, _l, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
         _lib = L
@@ -238,6 +241,28 @@ def quantize_v(v, head_dim=64):
     scales = np.zeros(v.shape[:-1], np.float32)
     lib().orc_quantize_v(_p(v), n_heads, head_dim, _p(codes), _p(scales))
     return codes, scales
+
+
+def fp8_table() -> np.ndarray:
+    """float32 [256]: the value of every e4m3 code (NaN for 0x7f, 0xff)."""
+    return np.array([lib().orc_fp8_value(c) for c in range(256)], np.float32)
+
+
+def quantize_fp8(x, head_dim=64):
+    """fp32 [..., n_heads, head_dim] -> (uint8 e4m3 codes, same shape; fp32 scales
+    [..., n_heads])."""
+    x = _f32(x)
+    n_heads = x.size // head_dim
+    codes = np.zeros(x.shape, np.uint8)
+    scales = np.zeros(x.shape[:-1], np.float32)
+    lib().orc_quantize_fp8(_p(x), n_heads, head_dim, _p(codes), _p(scales))
+    return codes, scales
+
+
+def dequantize_fp8(codes, scales):
+    """scale * value(code) in fp32, the values the e4m3 cache stands for."""
+    return (fp8_table()[np.asarray(codes, np.uint8)] *
+            np.asarray(scales, np.float32)[..., None]).astype(np.float32)
 
 
 def dequantize_v(codes, scales):

@@ -41,6 +41,16 @@ def v_block_offsets():
     return (d // 32) * 512 + ((t // 4) * 16 + d % 16) * 8 + ((d // 16) % 2) * 4 + t % 4
 
 
+def k_fp8_offsets(t):
+    """Byte offsets of dims 0..63 of token t in a head's 1 KB e4m3 K block: lane
+    kg*16 + t loads 16 bytes at lane*16, dims 8kg..8kg+7 then 32+8kg..+7."""
+    d = np.arange(D)
+    return ((d % 32) // 8 * 16 + t) * 16 + (d // 32) * 8 + d % 8
+
+
+FP8_NAN = 0x7F  # e4m3 NaN: the poison of slots that hold no token
+
+
 _K_OFF = k_block_offsets().reshape(-1)
 _V_OFF = v_block_offsets().reshape(-1)
 
@@ -63,9 +73,10 @@ def from_pool(p, kind):
 
 class DecodeCase:
     def __init__(self, B, n_q_heads, n_kv_heads, ctx_lens, window=0, scale=1.0, seed=0,
-                 extra_blocks=7, rope_rows=None, sink_scale=1.0, v_int8=False):
+                 extra_blocks=7, rope_rows=None, sink_scale=1.0, v_int8=False, kv_fp8=False):
         rng = np.random.default_rng(seed)
         self.v_int8 = v_int8
+        self.kv_fp8 = kv_fp8
         self.B, self.Hq, self.Hkv = B, n_q_heads, n_kv_heads
         self.window = window
         self.ring = window
@@ -96,7 +107,11 @@ class DecodeCase:
 
         # Caches, poisoned.
         self.k = np.full((self.num_blocks, n_kv_heads, BT, D), BF16_NAN, np.uint16)
-        if v_int8:
+        if kv_fp8:
+            self.k = np.full((self.num_blocks, n_kv_heads, BT * D), FP8_NAN, np.uint8)
+            self.v = np.full((self.num_blocks, n_kv_heads, BT * D), FP8_NAN, np.uint8)
+            self.vs = np.full((self.num_blocks, n_kv_heads, 2 * BT), np.nan, np.float32)
+        elif v_int8:
             self.v = np.full((self.num_blocks, n_kv_heads, BT * D), INT8_POISON, np.int8)
             self.vs = np.full((self.num_blocks, n_kv_heads, BT), np.nan, np.float32)
         else:
@@ -120,6 +135,15 @@ class DecodeCase:
             kh = O.to_bf16(rng.standard_normal((len(t_hist), n_kv_heads, D)) * scale)
             vf = (rng.standard_normal((len(t_hist), n_kv_heads, D)) * scale).astype(np.float32)
             slots = t_hist % self.ring if self.ring else t_hist
+            if kv_fp8:
+                kf = (rng.standard_normal((len(t_hist), n_kv_heads, D)) * scale).astype(np.float32)
+                kcodes, kscales = O.quantize_fp8(kf)
+                vcodes, vscales = O.quantize_fp8(vf)
+                self._place_f8(self.k, self.v, self.vs, b, slots, kcodes, kscales, vcodes,
+                               vscales)
+                self.kc[b, slots] = O.dequantize_fp8(kcodes, kscales)
+                self.vc[b, slots] = O.dequantize_fp8(vcodes, vscales)
+                continue
             if v_int8:
                 codes, scales = O.quantize_v(vf)
                 self._place_k(self.k, b, slots, kh)
@@ -132,16 +156,26 @@ class DecodeCase:
             self.kc[b, slots] = O.from_bf16(kh)
 
         # The append, per the oracle.
-        q_rot, _, kb, vb = O.kv_append(self.qkv, n_q_heads, n_kv_heads, self.cos, self.sin,
-                                       self.pos)
+        q_rot, k_rot, kb, vb = O.kv_append(self.qkv, n_q_heads, n_kv_heads, self.cos, self.sin,
+                                           self.pos)
         self.q_rot = q_rot
         self.k_expect = self.k.copy()
         self.v_expect = self.v.copy()
-        self.vs_expect = self.vs.copy() if v_int8 else None
+        self.vs_expect = self.vs.copy() if (v_int8 or kv_fp8) else None
         v_new = self.qkv[:, (n_q_heads + n_kv_heads) * D:].reshape(B, n_kv_heads, D)
+        k_new = np.asarray(k_rot, np.float32).reshape(B, n_kv_heads, D)
         for b in range(B):
             slot = int(self.pos[b] % self.ring) if self.ring else int(self.pos[b])
             phys = self.table[b, slot // BT]
+            if kv_fp8:
+                kcodes, kscales = O.quantize_fp8(k_new[b])
+                vcodes, vscales = O.quantize_fp8(v_new[b])
+                self._place_f8(self.k_expect, self.v_expect, self.vs_expect, b,
+                               np.array([slot]), kcodes[None], kscales[None], vcodes[None],
+                               vscales[None])
+                self.kc[b, slot] = O.dequantize_fp8(kcodes, kscales)
+                self.vc[b, slot] = O.dequantize_fp8(vcodes, vscales)
+                continue
             self.k_expect[phys, :, slot % BT, :] = kb[b]
             self.kc[b, slot] = O.from_bf16(kb[b])
             if v_int8:
@@ -165,6 +199,17 @@ class DecodeCase:
             t = int(slot % BT)
             v[phys][:, v_int8_offsets(t)] = codes[j]
             vs[phys, :, t] = scales[j]
+
+    def _place_f8(self, k, v, s, b, slots, kcodes, kscales, vcodes, vscales):
+        """e4m3 codes [n, Hkv, 64] and scales [n, Hkv] -> the e4m3 block layouts,
+        K scales at token t, V scales at 16 + t."""
+        for j, slot in enumerate(np.asarray(slots)):
+            phys = self.table[b, slot // BT]
+            t = int(slot % BT)
+            k[phys][:, k_fp8_offsets(t)] = kcodes[j]
+            v[phys][:, v_int8_offsets(t)] = vcodes[j]
+            s[phys, :, t] = kscales[j]
+            s[phys, :, BT + t] = vscales[j]
 
     def _place(self, b, slots, kh, vh):
         phys = self.table[b, slots // BT]
@@ -190,9 +235,10 @@ class DecodeCase:
             "pos": t(self.pos),
             "seq_lens": t(self.seq_lens),
             "table": t(self.table),
-            "k": t(to_pool(self.k, "k").view(np.int16)),
-            "v": t(self.v) if self.v_int8 else t(to_pool(self.v, "v").view(np.int16)),
-            "vs": t(self.vs) if self.v_int8 else None,
+            "k": t(self.k) if self.kv_fp8 else t(to_pool(self.k, "k").view(np.int16)),
+            "v": t(self.v) if (self.v_int8 or self.kv_fp8) else
+            t(to_pool(self.v, "v").view(np.int16)),
+            "vs": t(self.vs) if (self.v_int8 or self.kv_fp8) else None,
             "err": torch.zeros(1, dtype=torch.int32, device=device),
         }
         return dev

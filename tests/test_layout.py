@@ -8,7 +8,7 @@ from kvcase import from_pool, k_block_offsets, to_pool, v_block_offsets, v_int8_
 
 
 def test_layouts_are_permutations(gkv):
-    for kind in ("k", "v", "v_int8"):
+    for kind in ("k", "v", "v_int8", "k_fp8"):
         off = np.array(gkv.block_offsets(kind)).reshape(-1)
         assert sorted(off.tolist()) == list(range(1024)), kind
 
@@ -49,3 +49,13 @@ def test_pool_round_trip():
     # one element lands where the offset table says
     pk = to_pool(k, "k")
     assert pk[2, 3, k_block_offsets()[7, 45]] == k[2, 3, 7, 45]
+
+
+def test_k_fp8_lane_pieces(gkv):
+    """e4m3 K: lane kg*16 + t reads bytes lane*16 .. +15: dims 8kg..+7 of token t
+    (its first matrix-op piece), then dims 32+8kg..+7 (its second)."""
+    off = np.array(gkv.block_offsets("k_fp8"))    # [t][d] -> byte
+    for lane in range(64):
+        t, kg = lane % 16, lane // 16
+        want = [off[t, 8 * kg + j] for j in range(8)] + [off[t, 32 + 8 * kg + j] for j in range(8)]
+        assert want == list(range(lane * 16, lane * 16 + 16))

@@ -304,6 +304,79 @@ def test_quantize_v_matches_reference_build():
         assert np.array_equal(codes[0], rc) and np.float32(scales[0]) == np.float32(rs)
 
 
+# ---- e4m3 K/V cache (no reference counterpart) -------------------------------
+
+def test_fp8_table_closed_forms():
+    """The e4m3 format's fixed points: 1.0, the largest finite value, the
+    smallest normal and subnormal, NaN, monotone codes and sign symmetry."""
+    t = O.fp8_table()
+    assert t[0x38] == 1.0 and t[0x7E] == 448.0 and t[0x08] == 2.0 ** -6
+    assert t[0x01] == 2.0 ** -9 and t[0x00] == 0.0 and t[0x40] == 2.0
+    assert np.isnan(t[0x7F]) and np.isnan(t[0xFF])
+    pos = t[:0x7F]
+    assert (np.diff(pos) > 0).all()                # monotone in the code
+    assert np.array_equal(t[0x80:0xFF], -pos)      # sign bit
+    # within one binade 8 equal steps; subnormals continue the lowest one
+    assert np.allclose(np.diff(t[0x08:0x10]), 2.0 ** -9)
+    assert np.allclose(np.diff(t[0x00:0x09]), 2.0 ** -9)
+
+
+def _nearest_even_fp8(v, t):
+    """Brute force: the code whose value is nearest v, ties to the even code
+    (of v's sign for zero)."""
+    fin = np.array([c for c in range(256) if not np.isnan(t[c])])
+    d = np.abs(t[fin].astype(np.float64) - float(v))
+    cand = fin[d == d.min()]
+    if len(cand) > 1:
+        cand = [c for c in cand if c % 2 == 0 and bool(c & 0x80) == bool(np.signbit(v))] or cand
+    return int(cand[0])
+
+
+def test_quantize_fp8_is_nearest_even():
+    """Every code against a brute-force search of the table: random heads over
+    seven decades, every midpoint between neighbouring values (ties), and the
+    clamp edge."""
+    t = O.fp8_table()
+    rng = np.random.default_rng(21)
+    x = (rng.standard_normal((300, 64)) *
+         rng.choice([1e-6, 1e-3, 0.05, 1.0, 40.0, 1e4], (300, 1))).astype(np.float32)
+    codes, scales = O.quantize_fp8(x)
+    amax = np.abs(x).max(1)
+    assert np.array_equal(scales, (amax / np.float32(448.0)).astype(np.float32))
+    inv = (np.float32(448.0) / amax.astype(np.float32)).astype(np.float32)
+    c = np.clip((x * inv[:, None]).astype(np.float32), -448.0, 448.0)
+    for i in range(0, 300, 3):
+        for j in range(64):
+            assert codes[i, j] == _nearest_even_fp8(c[i, j], t), (c[i, j], codes[i, j])
+    # midpoints between neighbouring positive values, each scaled into a head
+    # whose amax is 448 (inv = 1, so the value itself is rounded)
+    pos = t[:0x7F].astype(np.float64)
+    mids = ((pos[:-1] + pos[1:]) / 2).astype(np.float32)
+    assert np.array_equal(mids.astype(np.float64), (pos[:-1] + pos[1:]) / 2)  # exact in fp32
+    for k in range(0, len(mids), 63):
+        chunk = mids[k:k + 63]
+        head = np.zeros(64, np.float32)
+        head[0] = 448.0
+        head[1:1 + len(chunk)] = chunk * np.where(np.arange(len(chunk)) % 2, -1, 1)
+        cc, sc = O.quantize_fp8(head.reshape(1, 64))
+        assert sc[0] == np.float32(1.0)
+        for j in range(64):
+            assert cc[0, j] == _nearest_even_fp8(head[j], t), (head[j], cc[0, j])
+    # the largest element of a head is exactly -448 here
+    h = np.array([[3.0, -7.5] + [0.1] * 62], np.float32)
+    cc, sc = O.quantize_fp8(h)
+    assert cc[0, 1] == 0xFE and sc[0] == np.float32(7.5) / np.float32(448.0)
+    inv = np.float32(448.0) / np.float32(7.5)
+    assert cc[0, 0] == _nearest_even_fp8(np.float32(3.0) * inv, t)
+    cc, sc = O.quantize_fp8(np.zeros((2, 64), np.float32))
+    assert not cc.any() and not sc.any()
+    # dequantized values stay within half a step of their binade
+    v = (rng.standard_normal((50, 64)) * 3).astype(np.float32)
+    cc, sc = O.quantize_fp8(v)
+    err = np.abs(O.dequantize_fp8(cc, sc) - v)
+    assert (err <= np.maximum(np.abs(v) * 2.0 ** -4, 2.0 ** -10 * sc[:, None]) * 1.0001).all()
+
+
 # ---- orc_linear (QKV projection: run.cpp matmul + bias add) ----------------
 
 def _bf16_values(a):
