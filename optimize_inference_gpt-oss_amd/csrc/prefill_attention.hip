@@ -78,7 +78,7 @@ struct PrefillArgs {
   int table_stride, num_blocks, ring;
   const float *sinks;
   int B, G, n_kv_heads, window, n_qblocks;
-  int group; // prompts whose query blocks are interleaved in the grid order
+  int band; // query blocks per band of the grid order
   void *out;
   int64_t out_stride;
   int out_bf16;
@@ -106,17 +106,20 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[2 * D * kVRow];
 
   // Grid order: kv head fastest (consecutive workgroups go to different
-  // XCDs, so each XCD holds the K/V of its own heads), then the prompts of a
-  // group of a.group prompts with their query blocks longest first (one
-  // group of all prompts by default: the longest blocks start first).
+  // XCDs, so each XCD holds the K/V of its own heads), then bands of a.band
+  // query blocks taken longest first, and in a band each prompt's blocks
+  // together: the blocks of one prompt-head that run side by side on one XCD
+  // share their K/V tiles in its L2 (a band's blocks see nearly the same
+  // keys), while the longest blocks still start first. Ids past the first
+  // query block (the last band's padding) exit at once.
   int id = blockIdx.x;
   const int g = id % a.n_kv_heads;
   id /= a.n_kv_heads;
-  const int span = a.group * a.n_qblocks;
-  const int grp = id / span, w = id - grp * span;
-  const int gs = min(a.group, a.B - grp * a.group); // prompts in this group
-  const int b = grp * a.group + w % gs;
-  const int qb = a.n_qblocks - 1 - w / gs;
+  const int band = id / (a.B * a.band), w = id - band * (a.B * a.band);
+  const int b = w / a.band;
+  const int qb = a.n_qblocks - 1 - (band * a.band + w % a.band);
+  if (qb < 0)
+    return;
   const int row0 = a.cu[b];
   const int L = a.cu[b + 1] - row0;
   const int q0 = qb * kQBlock;
@@ -531,17 +534,14 @@ static void launch_prefill(const gkv::PrefillArgs &a, int G, dim3 g, hipStream_t
     hipLaunchKernelGGL((prefill_kernel<1, HIST>), g, dim3(64), 0, s, a);
 }
 
-// Prompts per group of the grid order: all of them (every prompt's longest
-// block first), or GKV_PREFILL_GROUP (read once). Groups of 8 prompts cut
-// the HBM reads of config 4's full layer from 649 MB to 360 MB (the
-// algorithmic 351 MB) but lengthen the launch from 213 to 259 us: the
-// longest blocks of the last group start late.
-static int prompt_group(int B) {
+// Query blocks per band of the grid order (4, or GKV_PREFILL_BAND, read
+// once; 1 is the plain longest-first order).
+static int query_band() {
   static const int env = [] {
-    const char *e = getenv("GKV_PREFILL_GROUP");
-    return e ? atoi(e) : 0;
+    const char *e = getenv("GKV_PREFILL_BAND");
+    return e ? std::max(1, atoi(e)) : 4;
   }();
-  return env <= 0 ? std::max(B, 1) : std::min(env, std::max(B, 1));
+  return env;
 }
 
 static int prefill_launch(void *stream, int32_t B, const int32_t *cu_seqlens,
@@ -586,7 +586,8 @@ static int prefill_launch(void *stream, int32_t B, const int32_t *cu_seqlens,
           16 != 0)
     return GKV_ERR_ARG; // 16-byte vector loads
   const int n_qblocks = (max_len + kQBlock - 1) / kQBlock;
-  const int64_t grid = (int64_t)n_qblocks * B * n_kv_heads;
+  const int band = std::min(query_band(), std::max(n_qblocks, 1));
+  const int64_t grid = (int64_t)((n_qblocks + band - 1) / band) * band * B * n_kv_heads;
   if (grid == 0)
     return GKV_OK;
   if (grid >= INT32_MAX)
@@ -613,7 +614,7 @@ static int prefill_launch(void *stream, int32_t B, const int32_t *cu_seqlens,
   a.n_kv_heads = n_kv_heads;
   a.window = window;
   a.n_qblocks = n_qblocks;
-  a.group = prompt_group(B);
+  a.band = band;
   a.out = out;
   a.out_stride = out_stride;
   a.out_bf16 = out_dtype == GKV_BF16;
