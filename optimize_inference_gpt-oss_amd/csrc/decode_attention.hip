@@ -826,10 +826,8 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
   __shared__ int s_len[kMaxBatch];
   __shared__ int2 s_ids[kIdSlab / 2];
   __shared__ int s_rec[kInfoSlab];
-  __shared__ int s_ab[kInfoSlab]; // sequences whose new token lies in the range
   __shared__ int s_wave[kSplitWaves];
   __shared__ int s_max[kSplitWaves];
-  __shared__ int s_na;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nt = blockDim.x, B = a.B;
   const int n_waves = nt >> 6;
   const int w_id = blockIdx.x;
@@ -846,8 +844,6 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
     s_len[b] = L;
     s_cu[b] = pad_step(n);
   }
-  if (t == 0)
-    s_na = 0;
   __syncthreads();
   const int per = (B + nt - 1) / nt;
   const int b0 = min(t * per, B), b1 = min(b0 + per, B);
@@ -953,9 +949,42 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
   }
   const int n_steps = (re - rs) / kStep;
 
-  // Step records and block ids of the range. The table loads go out first;
-  // the list of new tokens in the range is published (LDS barrier, which does
-  // not wait for them) and the appends start while they are in flight.
+  // The new tokens in the range: the sequences that overlap it are a run of
+  // consecutive indices, each checked for its new token's place in the
+  // stream (its last position, or its ring slot). Wave w appends candidates
+  // w, w + 4, ...; the loads of its first go out now, before the step records'
+  // table loads, and it finishes after them.
+  int b_first = 0;
+  if (append) {
+    int lo = 0, hi = B - 1; // the sequence holding position rs: last b with cu[b] <= rs
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_cu[mid] <= rs)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    b_first = lo;
+  }
+  auto new_token_in_range = [&](int b) -> bool {
+    const int L = s_len[b];
+    int n = a.window > 0 ? min(L, a.window) : L;
+    n = max(min(n, min(a.table_stride * kBlockTokens, a.max_len)), 0);
+    const int slot = a.window > 0 ? (L - 1) % a.window : L - 1;
+    const int at = s_cu[b] + slot;
+    return L >= 1 && slot < n && at >= rs && at < re;
+  };
+  AppendLoads first_row;
+  int first_b = -1;
+  if (append) {
+    const int b = b_first + wave;
+    if (b < B && s_cu[b] < re && new_token_in_range(b)) {
+      first_row = append_begin(ap, b, lane, s_len[b] - 1);
+      first_b = b;
+    }
+  }
+
+  // Step records and block ids of the range (the table loads go out here).
   int id0[kStepsPerThread], id1[kStepsPerThread], rcd[kStepsPerThread];
 #pragma unroll
   for (int k = 0; k < kStepsPerThread; k++) {
@@ -983,22 +1012,20 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
       if (off + kBlockTokens < n)
         id1[k] = row[1];
       rcd[k] = step_record(b, off == 0, tok + kStep == s_cu[b + 1], min(max(n - off, 0), kStep));
-      if (append) {
-        // the new token's slot in the sequence's stream (position L - 1, or
-        // its ring slot)
-        const int slot = a.window > 0 ? (L - 1) % a.window : L - 1;
-        if (L >= 1 && slot < n && slot >= off && slot < off + kStep)
-          s_ab[atomicAdd(&s_na, 1)] = b;
-      }
     }
   }
-  lds_barrier();
 
   // The appends: one wave per new token, every kv head.
-  const int na = s_na;
-  for (int j = wave; j < na; j += n_waves) {
-    const int b = s_ab[j];
-    append_row(ap, b, lane, 0, 1, nullptr, s_len[b] - 1);
+  if (first_b >= 0)
+    append_end(ap, first_row, first_b, lane);
+  if (append) {
+    for (int j = wave + n_waves;; j += n_waves) {
+      const int b = b_first + j;
+      if (b >= B || s_cu[b] >= re)
+        break;
+      if (new_token_in_range(b))
+        append_row(ap, b, lane, 0, 1, nullptr, s_len[b] - 1);
+    }
   }
 
   bool any_bad = false;

@@ -69,6 +69,126 @@ __device__ __forceinline__ u32x4 pack8(const uint16_t *h) {
                h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16)};
 }
 
+// The key lanes' part of a row for kv head g, lane quarter j: rotate the
+// pairs (8j + i, 32 + 8j + i) of x1 (dims 8j..8j+7) and x2 (32+8j..), store
+// them into the cache (bf16 or e4m3) and the packed row.
+__device__ __forceinline__ void append_keys(const AppendArgs &a, int r, int g, int j,
+                                            const f32x4 (&x1)[2], const f32x4 (&x2)[2],
+                                            const f32x4 (&c)[2], const f32x4 (&s)[2],
+                                            bool store, int64_t kbase, int off) {
+  constexpr int D = kHeadDim, HALF = kHeadDim / 2;
+  const int kv_dim = a.n_kv_heads * D;
+  float f1[8], f2[8];
+  uint16_t o1[8], o2[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float a1 = x1[i / 4][i % 4], a2 = x2[i / 4][i % 4];
+    const float cc = c[i / 4][i % 4], ss = s[i / 4][i % 4];
+    f1[i] = rope_first(a1, a2, cc, ss);
+    f2[i] = rope_second(a1, a2, cc, ss);
+    o1[i] = f32_to_bf16_rne(f1[i]);
+    o2[i] = f32_to_bf16_rne(f2[i]);
+  }
+  const u32x4 p1 = pack8(o1), p2 = pack8(o2);
+  if (store && a.kv_fp8) {
+    // e4m3 K: the head's max |k| over its 4 lanes, then one scale per
+    // token and head; the lane's 16 codes are one 16-byte piece
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      amax = fmaxf(amax, fmaxf(fabsf(f1[i]), fabsf(f2[i])));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+    const u32x4 w{fp8x4(f1[0], f1[1], f1[2], f1[3], inv), fp8x4(f1[4], f1[5], f1[6], f1[7], inv),
+                  fp8x4(f2[0], f2[1], f2[2], f2[3], inv), fp8x4(f2[4], f2[5], f2[6], f2[7], inv)};
+    const int64_t hb = kbase + (int64_t)g * (kBlockTokens * D); // bytes: 1 KB per head
+    *(u32x4 *)((uint8_t *)a.kc + hb + k_fp8_offset(off, 8 * j)) = w;
+    if (j == 0)
+      a.vs[hb / 32 + off] = amax / 448.0f;
+  } else if (store) {
+    uint16_t *kd = a.kc + kbase + (int64_t)g * (kBlockTokens * D);
+    *(u32x4 *)(kd + k_offset(off, 8 * j)) = p1;
+    *(u32x4 *)(kd + k_offset(off, HALF + 8 * j)) = p2;
+  }
+  if (a.k_pack) {
+    uint16_t *kp = a.k_pack + (int64_t)r * kv_dim + g * D;
+    *(u32x4 *)(kp + 8 * j) = p1;
+    *(u32x4 *)(kp + HALF + 8 * j) = p2;
+  }
+}
+
+// The value lanes' part of a row for kv head g, quarter q (dims 16q ..
+// 16q+15 in x): the packed row, then the cache (bf16, int8 or e4m3), or the
+// bf16 values into v_stage for the caller to store.
+__device__ __forceinline__ void append_values(const AppendArgs &a, int r, int g, int q,
+                                              const f32x4 (&x)[4], bool store, int64_t vbase,
+                                              int off, uint16_t *v_stage) {
+  constexpr int D = kHeadDim;
+  const int kv_dim = a.n_kv_heads * D;
+  uint16_t h[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++)
+    h[i] = f32_to_bf16_rne(x[i / 4][i % 4]);
+  if (a.v_pack) {
+    uint16_t *vpk = a.v_pack + (int64_t)r * kv_dim + g * D + 16 * q;
+    *(u32x4 *)vpk = pack8(h);
+    *(u32x4 *)(vpk + 8) = pack8(h + 8);
+  }
+  if (v_stage && !a.v_int8 && !a.kv_fp8) {
+    *(u32x4 *)(v_stage + g * D + 16 * q) = pack8(h);
+    *(u32x4 *)(v_stage + g * D + 16 * q + 8) = pack8(h + 8);
+    return;
+  }
+  if (!store)
+    return;
+  if (a.kv_fp8) {
+    // e4m3 V: the head's max |v| over its 4 lanes, one scale per token and
+    // head (after the token's K scale), codes in the int8 V layout
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+      amax = fmaxf(amax, fabsf(x[i / 4][i % 4]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+    const int64_t hb = vbase + (int64_t)g * (kBlockTokens * D); // bytes: 1 KB per head
+    uint8_t *vq = (uint8_t *)a.vc + hb;
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      const uint32_t w = fp8x4(x[i / 4][0], x[i / 4][1], x[i / 4][2], x[i / 4][3], inv);
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+        vq[v_int8_offset(16 * q + i + k, off)] = (uint8_t)(w >> (8 * k));
+    }
+    if (q == 0)
+      a.vs[hb / 32 + kBlockTokens + off] = amax / 448.0f;
+  } else if (a.v_int8) {
+    // The head's max |v| over its 4 lanes, then the reference's rule,
+    // getp-csrc/kernels/fast_misc.hpp:74-84.
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+      amax = fmaxf(amax, fabsf(x[i / 4][i % 4]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+    int8_t *vq = (int8_t *)a.vc + vbase + (int64_t)g * (kBlockTokens * D);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float c = fminf(fmaxf(rintf(x[i / 4][i % 4] * inv), -127.0f), 127.0f);
+      vq[v_int8_offset(16 * q + i, off)] = (int8_t)c;
+    }
+    if (q == 0)
+      a.vs[vbase / D + (int64_t)g * kBlockTokens + off] = amax / 127.0f;
+  } else {
+    uint16_t *vd = a.vc + vbase + (int64_t)g * (kBlockTokens * D);
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+      vd[v_offset(off, 16 * q + i)] = h[i];
+  }
+}
+
 // Row r of the call, by one wave (lane = 0..63). Lanes 0-31 take the keys:
 // lane (g, j) of head g = lane / 4 rotates the pairs (8j + i, 32 + 8j + i),
 // i = 0..7, and stores dims 8j..8j+7 and 32+8j..32+8j+7 as two 16-byte pieces
@@ -150,44 +270,7 @@ __device__ __forceinline__ RowPlace append_row(const AppendArgs &a, int r, int l
       const f32x4 *cp = (const f32x4 *)(cs + 8 * j), *sp = (const f32x4 *)(sn + 8 * j);
       const f32x4 x1[2] = {k1p[0], k1p[1]}, x2[2] = {k2p[0], k2p[1]};
       const f32x4 c[2] = {cp[0], cp[1]}, s[2] = {sp[0], sp[1]};
-      float f1[8], f2[8];
-      uint16_t o1[8], o2[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float a1 = x1[i / 4][i % 4], a2 = x2[i / 4][i % 4];
-        const float cc = c[i / 4][i % 4], ss = s[i / 4][i % 4];
-        f1[i] = rope_first(a1, a2, cc, ss);
-        f2[i] = rope_second(a1, a2, cc, ss);
-        o1[i] = f32_to_bf16_rne(f1[i]);
-        o2[i] = f32_to_bf16_rne(f2[i]);
-      }
-      const u32x4 p1 = pack8(o1), p2 = pack8(o2);
-      if (store && a.kv_fp8) {
-        // e4m3 K: the head's max |k| over its 4 lanes, then one scale per
-        // token and head; the lane's 16 codes are one 16-byte piece
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-          amax = fmaxf(amax, fmaxf(fabsf(f1[i]), fabsf(f2[i])));
-        amax = fmaxf(amax, __shfl_xor(amax, 1));
-        amax = fmaxf(amax, __shfl_xor(amax, 2));
-        const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
-        const u32x4 w{fp8x4(f1[0], f1[1], f1[2], f1[3], inv), fp8x4(f1[4], f1[5], f1[6], f1[7], inv),
-                      fp8x4(f2[0], f2[1], f2[2], f2[3], inv), fp8x4(f2[4], f2[5], f2[6], f2[7], inv)};
-        const int64_t hb = kbase + (int64_t)g * (kBlockTokens * D); // bytes: 1 KB per head
-        *(u32x4 *)((uint8_t *)a.kc + hb + k_fp8_offset(off, 8 * j)) = w;
-        if (j == 0)
-          a.vs[hb / 32 + off] = amax / 448.0f;
-      } else if (store) {
-        uint16_t *kd = a.kc + kbase + (int64_t)g * (kBlockTokens * D);
-        *(u32x4 *)(kd + k_offset(off, 8 * j)) = p1;
-        *(u32x4 *)(kd + k_offset(off, HALF + 8 * j)) = p2;
-      }
-      if (a.k_pack) {
-        uint16_t *kp = a.k_pack + (int64_t)r * kv_dim + g * D;
-        *(u32x4 *)(kp + 8 * j) = p1;
-        *(u32x4 *)(kp + HALF + 8 * j) = p2;
-      }
+      append_keys(a, r, g, j, x1, x2, c, s, store, kbase, off);
     }
     return place;
   }
@@ -195,69 +278,88 @@ __device__ __forceinline__ RowPlace append_row(const AppendArgs &a, int r, int l
     const int q = lane % 4;
     const f32x4 *vp = (const f32x4 *)(vr + g * D + 16 * q);
     const f32x4 x[4] = {vp[0], vp[1], vp[2], vp[3]};
-    uint16_t h[16];
-#pragma unroll
-    for (int i = 0; i < 16; i++)
-      h[i] = f32_to_bf16_rne(x[i / 4][i % 4]);
-    if (a.v_pack) {
-      uint16_t *vpk = a.v_pack + (int64_t)r * kv_dim + g * D + 16 * q;
-      *(u32x4 *)vpk = pack8(h);
-      *(u32x4 *)(vpk + 8) = pack8(h + 8);
-    }
-    if (v_stage && !a.v_int8 && !a.kv_fp8) {
-      *(u32x4 *)(v_stage + g * D + 16 * q) = pack8(h);
-      *(u32x4 *)(v_stage + g * D + 16 * q + 8) = pack8(h + 8);
-      continue;
-    }
-    if (!store)
-      continue;
-    if (a.kv_fp8) {
-      // e4m3 V: the head's max |v| over its 4 lanes, one scale per token and
-      // head (after the token's K scale), codes in the int8 V layout
-      float amax = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 16; i++)
-        amax = fmaxf(amax, fabsf(x[i / 4][i % 4]));
-      amax = fmaxf(amax, __shfl_xor(amax, 1));
-      amax = fmaxf(amax, __shfl_xor(amax, 2));
-      const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
-      const int64_t hb = vbase + (int64_t)g * (kBlockTokens * D); // bytes: 1 KB per head
-      uint8_t *vq = (uint8_t *)a.vc + hb;
-#pragma unroll
-      for (int i = 0; i < 16; i += 4) {
-        const uint32_t w = fp8x4(x[i / 4][0], x[i / 4][1], x[i / 4][2], x[i / 4][3], inv);
-#pragma unroll
-        for (int k = 0; k < 4; k++)
-          vq[v_int8_offset(16 * q + i + k, off)] = (uint8_t)(w >> (8 * k));
-      }
-      if (q == 0)
-        a.vs[hb / 32 + kBlockTokens + off] = amax / 448.0f;
-    } else if (a.v_int8) {
-      // The head's max |v| over its 4 lanes, then the reference's rule,
-      // getp-csrc/kernels/fast_misc.hpp:74-84.
-      float amax = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 16; i++)
-        amax = fmaxf(amax, fabsf(x[i / 4][i % 4]));
-      amax = fmaxf(amax, __shfl_xor(amax, 1));
-      amax = fmaxf(amax, __shfl_xor(amax, 2));
-      const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
-      int8_t *vq = (int8_t *)a.vc + vbase + (int64_t)g * (kBlockTokens * D);
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const float c = fminf(fmaxf(rintf(x[i / 4][i % 4] * inv), -127.0f), 127.0f);
-        vq[v_int8_offset(16 * q + i, off)] = (int8_t)c;
-      }
-      if (q == 0)
-        a.vs[vbase / D + (int64_t)g * kBlockTokens + off] = amax / 127.0f;
-    } else {
-      uint16_t *vd = a.vc + vbase + (int64_t)g * (kBlockTokens * D);
-#pragma unroll
-      for (int i = 0; i < 16; i++)
-        vd[v_offset(off, 16 * q + i)] = h[i];
-    }
+    append_values(a, r, g, q, x, store, vbase, off, v_stage);
   }
   return place;
+}
+
+// A row's append in two halves, for a caller that overlaps the row's loads
+// with other work: append_begin issues the loads (the placement's table
+// entry, the lane's K or V pieces, the angles), append_end rotates, rounds and
+// stores, as append_row does. One wave per row, at most 8 kv heads, no
+// rotated-query output; the caller knows the row's position.
+struct AppendLoads {
+  int seq, slot, off, table_entry; // table_entry: the block id as loaded (-1: none)
+  bool store;
+  f32x4 x[4];  // key lanes: dims 8j..8j+7, then 32+8j..+7; value lanes: dims 16q..16q+15
+  f32x4 cs[4]; // key lanes: the cos, then the sin of those pairs
+};
+
+__device__ __forceinline__ AppendLoads append_begin(const AppendArgs &a, int r, int lane,
+                                                    int pos) {
+  constexpr int D = kHeadDim, HALF = kHeadDim / 2;
+  AppendLoads L;
+  L.seq = a.row_seq ? a.row_seq[r] : r;
+  L.slot = a.ring > 0 ? pos % a.ring : pos;
+  L.off = L.slot % kBlockTokens;
+  L.store = a.kc != nullptr;
+  if (L.store && a.ring > 0 && a.seq_lens && pos + a.ring < a.seq_lens[L.seq])
+    L.store = false; // a later row of this call takes the ring slot
+  const int blk = L.slot / kBlockTokens;
+  L.table_entry = L.store && blk < a.table_stride
+                      ? a.table[(int64_t)L.seq * a.table_stride + blk]
+                      : -1;
+  // The same four loads on every lane (no divergent branch, so the loaded
+  // registers are not merged through memory): a key lane's dims 8j..+7 and
+  // 32+8j..+7, a value lane's 16q..16q+15; lanes past the heads re-read the
+  // last head.
+  const float *row = a.qkv + (int64_t)r * a.row_stride;
+  const int g = min((lane & 31) / 4, a.n_kv_heads - 1), j = lane % 4;
+  const bool key = lane < 32;
+  const float *xp = row + a.n_q_heads * D + (key ? 0 : a.n_kv_heads * D) + g * D +
+                    (key ? 8 * j : 16 * j);
+  const int second = key ? HALF : 8;
+  L.x[0] = *(const f32x4 *)xp;
+  L.x[1] = *(const f32x4 *)(xp + 4);
+  L.x[2] = *(const f32x4 *)(xp + second);
+  L.x[3] = *(const f32x4 *)(xp + second + 4);
+  const float *cp = a.cos_tab + (int64_t)pos * HALF + 8 * j;
+  const float *sp = a.sin_tab + (int64_t)pos * HALF + 8 * j;
+  L.cs[0] = *(const f32x4 *)cp;
+  L.cs[1] = *(const f32x4 *)(cp + 4);
+  L.cs[2] = *(const f32x4 *)sp;
+  L.cs[3] = *(const f32x4 *)(sp + 4);
+  return L;
+}
+
+__device__ __forceinline__ void append_end(const AppendArgs &a, const AppendLoads &L, int r,
+                                           int lane) {
+  constexpr int D = kHeadDim;
+  bool store = L.store;
+  int64_t base = 0;
+  if (store) {
+    if (L.slot / kBlockTokens >= a.table_stride) {
+      if (lane == 0 && a.dev_err)
+        atomicOr(a.dev_err, GKV_DEVERR_LENGTH);
+      store = false;
+    } else if (L.table_entry < 0 || L.table_entry >= a.num_blocks) {
+      if (lane == 0 && a.dev_err)
+        atomicOr(a.dev_err, GKV_DEVERR_BLOCK_ID);
+      store = false;
+    } else {
+      base = (int64_t)L.table_entry * a.n_kv_heads * (kBlockTokens * D);
+    }
+  }
+  const int g = (lane & 31) / 4, j = lane % 4;
+  if (g >= a.n_kv_heads)
+    return;
+  if (lane < 32) {
+    const f32x4 x1[2] = {L.x[0], L.x[1]}, x2[2] = {L.x[2], L.x[3]};
+    const f32x4 c[2] = {L.cs[0], L.cs[1]}, s[2] = {L.cs[2], L.cs[3]};
+    append_keys(a, r, g, j, x1, x2, c, s, store, base, L.off);
+  } else {
+    append_values(a, r, g, j, L.x, store, base, L.off, nullptr);
+  }
 }
 
 } // namespace gkv
