@@ -947,6 +947,12 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
       return;
     re = min(rs + S, T);
   }
+  // The range is the same for every lane; saying so keeps the stream's
+  // addresses in scalar registers (a bound the compiler takes for divergent,
+  // e.g. one that went through a cross-lane max, makes every load of the
+  // stream a loop over lanes).
+  rs = uniform(rs);
+  re = uniform(re);
   const int n_steps = (re - rs) / kStep;
 
   // The new tokens in the range: the sequences that overlap it are a run of
