@@ -282,16 +282,58 @@ __global__ __launch_bounds__(64 * kNW) void qkv_append_kernel(QkvArgs a) {
       const bool st_ok = m0 + lr < a.M && off >= 0;
       if (is_k) {
         const int pos = s_pos[lr];
+        float kr[4]; // dims n, 16 + n (first of their pairs), 32 + n, 48 + n
 #pragma unroll
         for (int j = 0; j < 2; j++) { // dims d = 16 j + n and d + 32
           const int d = 16 * j + n;
           const float c = ap.cos_tab[(int64_t)pos * HALF + d];
           const float s = ap.sin_tab[(int64_t)pos * HALF + d];
           const float x1 = acc[i][j][r], x2 = acc[i][j + 2][r];
+          kr[j] = rope_first(x1, x2, c, s);
+          kr[j + 2] = rope_second(x1, x2, c, s);
+        }
+        if (ap.kv_fp8) {
+          // e4m3 K: the head's max |k| over its 64 dims (16 lanes), one
+          // scale per token and head, each code stored by its lane
+          float amax = 0.0f;
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+            amax = fmaxf(amax, fabsf(kr[j]));
+#pragma unroll
+          for (int sh = 1; sh < 16; sh <<= 1)
+            amax = fmaxf(amax, __shfl_xor(amax, sh));
+          const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
           if (st_ok) {
-            ap.kc[base + k_offset(off, d)] = f32_to_bf16_rne(rope_first(x1, x2, c, s));
-            ap.kc[base + k_offset(off, d + HALF)] = f32_to_bf16_rne(rope_second(x1, x2, c, s));
+            uint8_t *kq = (uint8_t *)ap.kc + base;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+              kq[k_fp8_offset(off, 16 * j + n)] = (uint8_t)fp8x4(kr[j], 0.0f, 0.0f, 0.0f, inv);
+            if (n == 0)
+              ap.vs[base / 32 + off] = amax / 448.0f;
           }
+        } else if (st_ok) {
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+            ap.kc[base + k_offset(off, 16 * j + n)] = f32_to_bf16_rne(kr[j]);
+        }
+      } else if (ap.kv_fp8) {
+        // e4m3 V: as the key, codes in the int8 V layout, the scale after
+        // the token's K scale
+        float amax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          amax = fmaxf(amax, fabsf(acc[i][j][r]));
+#pragma unroll
+        for (int sh = 1; sh < 16; sh <<= 1)
+          amax = fmaxf(amax, __shfl_xor(amax, sh));
+        const float inv = amax > 0.0f ? 448.0f / amax : 0.0f;
+        if (st_ok) {
+          uint8_t *vq = (uint8_t *)ap.vc + base;
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+            vq[v_int8_offset(16 * j + n, off)] = (uint8_t)fp8x4(acc[i][j][r], 0.0f, 0.0f, 0.0f, inv);
+          if (n == 0)
+            ap.vs[base / 32 + kBlockTokens + off] = amax / 448.0f;
         }
       } else if (ap.v_int8) {
         // the head's max |v| over its 64 dims (4 per lane, 16 lanes), then
@@ -356,11 +398,10 @@ extern "C" int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64
     return GKV_ERR_ARG; // rows W positions apart share a ring slot: the lengths pick the kept one
   if (cache.ring % kBlockTokens != 0)
     return GKV_ERR_UNSUPPORTED;
-  if (cache.v_format == GKV_KV_FP8)
-    return GKV_ERR_UNSUPPORTED; // the epilogue stores bf16 K (gkv_kv_append stores e4m3)
-  if (cache.v_format != GKV_V_BF16 && cache.v_format != GKV_V_INT8)
+  if (cache.v_format != GKV_V_BF16 && cache.v_format != GKV_V_INT8 &&
+      cache.v_format != GKV_KV_FP8)
     return GKV_ERR_ARG;
-  if (to_cache && cache.v_format == GKV_V_INT8 && !cache.v_scale)
+  if (to_cache && cache.v_format != GKV_V_BF16 && !cache.v_scale)
     return GKV_ERR_ARG;
   if (n_rows == 0)
     return GKV_OK;
@@ -404,7 +445,7 @@ extern "C" int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64
   ap.v_pack = nullptr;
   ap.dev_err = dev_err;
   ap.v_int8 = cache.v_format == GKV_V_INT8;
-  ap.kv_fp8 = 0;
+  ap.kv_fp8 = cache.v_format == GKV_KV_FP8;
   ap.vs = (float *)cache.v_scale;
   if (big)
     hipLaunchKernelGGL(

@@ -147,17 +147,18 @@ def test_decode_argument_checks(gkv):
 
 
 def test_fp8_cache_where_unsupported(gkv):
-    """The e4m3 cache is read by the decode path only: the prefill over a
-    history and the QKV projection's epilogue reject it."""
+    """The prefill over a history rejects the e4m3 cache; the appends need its
+    scales."""
     L = gkv.lib()
     fake = 0x1000
     view = gkv.CacheView(fake, fake, fake, 8, 64, 8, 0, fake, gkv.KV_FP8)
     st = L.gkv_prefill_paged(None, 1, fake, fake, 32, 64, fake, 5120, fake, fake, None, None,
                              view, fake, 0, fake, 4096, 0, None)
     assert st == gkv.GKV_ERR_UNSUPPORTED
+    noscale = gkv.CacheView(fake, fake, fake, 8, 64, 8, 0, None, gkv.KV_FP8)
     st = L.gkv_qkv_append(None, 4, fake, 2880, 2880, fake, None, 64, fake, fake, None, None,
-                          fake, view, fake, 5120, None)
-    assert st == gkv.GKV_ERR_UNSUPPORTED
+                          fake, noscale, fake, 5120, None)
+    assert st == gkv.GKV_ERR_ARG  # the e4m3 cache needs its scales
     bad = gkv.CacheView(fake, fake, fake, 8, 64, 8, 0, None, gkv.KV_FP8)  # scales required
     st = L.gkv_kv_append(None, 4, fake, 5120, 64, fake, fake, fake, None, fake, bad, None, 0,
                          None, None, None)

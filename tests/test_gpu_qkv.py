@@ -33,9 +33,11 @@ class QkvCase:
     Decode mode (prompts=None): row b is sequence b at position lens[b]-1.
     Prompt mode: rows are every position of each prompt (row_pos, row_seq)."""
 
-    def __init__(self, seed, Hq, Hkv, hidden, lens=None, prompts=None, window=0, v_int8=False):
+    def __init__(self, seed, Hq, Hkv, hidden, lens=None, prompts=None, window=0, v_int8=False,
+                 kv_fp8=False):
         rng = np.random.default_rng(seed)
         self.Hq, self.Hkv, self.hidden, self.window, self.v_int8 = Hq, Hkv, hidden, window, v_int8
+        self.kv_fp8 = kv_fp8
         self.N = (Hq + 2 * Hkv) * D
         if prompts is None:
             self.lens = np.asarray(lens, np.int32)
@@ -73,6 +75,12 @@ def run(case, gkv, torch, dev, cache=True):
     table = t(case.table)
 
     def new_cache():
+        if case.kv_fp8:  # e4m3 codes poisoned with the NaN code, scales with NaN
+            k = t(np.full((case.NB, case.Hkv, 16 * D), 0x7F, np.uint8))
+            v = t(np.full((case.NB, case.Hkv, 16 * D), 0x7F, np.uint8))
+            vs = t(np.full((case.NB, case.Hkv, 32), np.nan, np.float32))
+            return k, v, vs, gkv.cache_view(k, v, table, case.Hkv, ring=case.window, v_scale=vs,
+                                            v_format=gkv.KV_FP8)
         k = t(np.full((case.NB, case.Hkv, 16, D), NAN16, np.uint16).view(np.int16))
         vs = None
         if case.v_int8:
@@ -100,7 +108,7 @@ def run(case, gkv, torch, dev, cache=True):
     res = dict(err=int(err.item()), qkv=qkv_out.cpu().numpy(),
                k1=k1.cpu().numpy(), v1=v1.cpu().numpy(), k2=k2.cpu().numpy(),
                v2=v2.cpu().numpy(), cos=cos, sin=sin)
-    if case.v_int8:
+    if case.v_int8 or case.kv_fp8:
         res["vs1"], res["vs2"] = vs1.cpu().numpy(), vs2.cpu().numpy()
     return res
 
@@ -115,7 +123,38 @@ def check_projection(case, res, oracle, rows=None):
     assert not bad.any(), f"{int(bad.sum())} projections out of bound, max err {err.max()}"
 
 
+def check_cache_fp8(case, res, oracle):
+    """e4m3 K/V: every byte and scale equal to gkv_kv_append's, and the codes
+    and scales of each stored row equal to the oracle's quantizer on the
+    oracle's rotated key and on the value."""
+    from kvcase import k_fp8_offsets, v_int8_offsets
+    for a, b in (("k1", "k2"), ("v1", "v2")):
+        assert np.array_equal(res[a], res[b]), f"{a} differs from gkv_kv_append's"
+    assert np.array_equal(res["vs1"].view(np.uint32), res["vs2"].view(np.uint32)), "scales differ"
+    _, k_rot, _, _ = oracle.kv_append(res["qkv"], case.Hq, case.Hkv, res["cos"], res["sin"],
+                                      case.row_pos)
+    v_rows = res["qkv"][:, (case.Hq + case.Hkv) * D:].reshape(case.M, case.Hkv, D)
+    kc, ks = oracle.quantize_fp8(np.asarray(k_rot, np.float32).reshape(case.M, case.Hkv, D))
+    vc, vsc = oracle.quantize_fp8(v_rows)
+    n_checked = 0
+    for r in range(case.M):
+        b, p = int(case.row_seq[r]), int(case.row_pos[r])
+        if case.window and p + case.window < case.lens[b]:
+            continue
+        slot = p % case.window if case.window else p
+        phys, off = case.table[b, slot // 16], slot % 16
+        assert np.array_equal(res["k1"][phys][:, k_fp8_offsets(off)], kc[r]), f"K of row {r}"
+        assert np.array_equal(res["v1"][phys][:, v_int8_offsets(off)], vc[r]), f"V of row {r}"
+        assert np.array_equal(res["vs1"][phys, :, off].view(np.uint32), ks[r].view(np.uint32))
+        assert np.array_equal(res["vs1"][phys, :, 16 + off].view(np.uint32),
+                              vsc[r].view(np.uint32))
+        n_checked += 1
+    assert n_checked > 0
+
+
 def check_cache(case, res, oracle):
+    if case.kv_fp8:
+        return check_cache_fp8(case, res, oracle)
     assert np.array_equal(res["k1"], res["k2"]), "K cache bytes differ from gkv_kv_append's"
     assert np.array_equal(res["v1"], res["v2"]), "V cache bytes differ from gkv_kv_append's"
     if case.v_int8:
@@ -181,6 +220,18 @@ def test_int8_v(oracle, gkv, cuda):
     assert res["err"] == 0
     check_projection(case, res, oracle)
     check_cache(case, res, oracle)
+
+
+def test_fp8_kv(oracle, gkv, cuda):
+    """The e4m3 K/V cache from the projection's epilogue: decode rows on a full
+    layer and prompt rows (the 128 x 128 tiles) on a ring."""
+    import torch
+    rng = np.random.default_rng(31)
+    for case in (QkvCase(32, 16, 4, 512, lens=rng.integers(1, 300, 100), kv_fp8=True),
+                 QkvCase(33, 64, 8, 2880, prompts=[900, 700, 500], window=128, kv_fp8=True)):
+        res = run(case, gkv, torch, cuda)
+        assert res["err"] == 0
+        check_cache(case, res, oracle)
 
 
 @pytest.mark.parametrize("hidden", [64, 128, 192])
