@@ -554,6 +554,9 @@ def main() -> int:
     ap.add_argument("--separate-append", action="store_true",
                     help="append with gkv_kv_append, then gkv_decode_attention (four launches "
                          "per layer instead of gkv_decode_layer's three)")
+    ap.add_argument("--no-plan-reuse", action="store_true",
+                    help="several layers: every layer plans (gkv_decode_layer) instead of the "
+                         "first of each kind keeping its plan and the others reusing it")
     ap.add_argument("--prefill-from-cache", action="store_true",
                     help="config 4: the full layer's append writes the paged cache only and the "
                          "prefill reads every key from it (gkv_prefill_paged) instead of from "
@@ -624,7 +627,10 @@ def main() -> int:
     lens_d = torch.from_numpy(seq_lens).to(dev)
     err_d = torch.zeros(1, dtype=torch.int32, device=dev)
     ws_bytes = max(gkv.workspace_bytes(B, Hkv, max_len, 0, args.split_tokens), 4)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    # one workspace per layer kind (full, window): a kind's later layers reuse
+    # the plan its first layer keeps there
+    ws_of = {w: torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+             for w in sorted({l.window for l in layers})}
     stream = torch.cuda.current_stream()
 
     # algorithmic bytes per cached token and kv head: K bf16 (128 B) + V bf16
@@ -657,6 +663,15 @@ def main() -> int:
     # sequences (window layers); the step then skips it too
     combines = [args.staged or args.separate_append or
                 gkv.layer_combines(B, Hkv, max_len, l.window, args.split_tokens) for l in layers]
+    # Default, with several layers: the first layer of each kind in a step
+    # keeps its plan (gkv_decode_layer_split_planned, GKV_PLAN_KEEP), the
+    # others of that kind reuse it (GKV_PLAN_REUSE).
+    plan_of = [None] * n_layers
+    if stages[0] == "append+split" and n_layers > 1 and not args.no_plan_reuse:
+        seen = set()
+        for li, layer in enumerate(layers):
+            plan_of[li] = gkv.PLAN_REUSE if layer.window in seen else gkv.PLAN_KEEP
+            seen.add(layer.window)
 
     def step(record: bool):
         for li, layer in enumerate(layers):
@@ -670,6 +685,14 @@ def main() -> int:
                                   seq_lens=lens_d, dev_err=err_d, stream=stream)
                     continue
                 if stage == "combine" and not combines[li]:
+                    continue
+                ws = ws_of[layer.window]
+                if stage == "append+split" and plan_of[li] is not None:
+                    gkv.decode_layer_planned(layer.qkv, lens_d, max_len, layer.view, layer.sinks,
+                                             layer.out, cos_d, sin_d, plan_of[li],
+                                             window=layer.window,
+                                             split_tokens=args.split_tokens, workspace=ws,
+                                             dev_err=err_d, stream=stream, split_only=True)
                     continue
                 api = {"append+prepare": "layer_prepare",
                        "append+split": "layer_split"}.get(stage, stage)
@@ -757,6 +780,8 @@ def main() -> int:
             "context": f"U[{cfg['lo']},{cfg['hi']}]", "window": cfg["window"],
             "kv_bytes_per_step": kv_bytes, "v_cache": "fp8 K and V (e4m3) + scales" if args.kv_fp8 else "int8+scale" if args.v_int8 else "bf16", "split_tokens": args.split_tokens or "balanced",
             "pool_bytes": pool.device_bytes(),
+            "plan": "kept by each kind's first layer, reused by the others"
+                    if plan_of[-1] is not None else "every layer plans",
             "kernel_ms": dict(zip(stages, (round(float(x), 4) for x in stage_ms))),
             "parallelism": "1 GPU",
         },

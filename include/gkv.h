@@ -70,6 +70,8 @@ typedef enum {
 #define GKV_DEVERR_ALIGN 4u    /* a prefill start position that is not a multiple of 16 */
 #define GKV_DEVERR_RANGE 8u    /* a V beyond the prefill's range (|v| >= 2^26: the output
                                   holds inf there) */
+#define GKV_DEVERR_PLAN 16u    /* gkv_decode_layer_planned was asked to reuse a plan the
+                                  workspace does not hold for this call (it planned afresh) */
 
 typedef enum { GKV_F32 = 0, GKV_BF16 = 1 } gkv_dtype;
 
@@ -268,6 +270,41 @@ int gkv_decode_layer_prepare(void *stream, int32_t B, int32_t n_q_heads, const f
                              int32_t window, const float *sinks, int32_t split_tokens,
                              void *workspace, size_t workspace_bytes, void *out,
                              int64_t out_stride, int32_t out_dtype, uint32_t *dev_err);
+
+/* gkv_decode_layer for the engine's loop over layers
+ * (getp-csrc/engine/gpu_engine.hpp:652, layer_attention per layer at :495-498):
+ * the layers of one kind (full, or sliding window) in one decode step share
+ * the lengths and the block table, so the split launch's plan (the ranges,
+ * the step records and block ids) is the same for all of them. plan =
+ * GKV_PLAN_KEEP plans as gkv_decode_layer does and keeps the plan in the
+ * workspace; GKV_PLAN_REUSE takes the kept plan instead of planning (the
+ * prologue then only loads it and appends). GKV_PLAN_NONE is gkv_decode_layer.
+ * Results are bit-identical to gkv_decode_layer's. Reuse needs the same
+ * workspace, seq_lens and block_table pointers, B, window, split_tokens,
+ * max_seq_len and pool shape as the keeping call, and unchanged lengths and
+ * table contents; a launch that plans afresh on the workspace (any other
+ * decode entry point) drops the kept plan. A key in the workspace checks the
+ * shape and pointers: on a mismatch the call plans afresh and sets
+ * GKV_DEVERR_PLAN; changed contents are not detected. Length errors
+ * (GKV_DEVERR_LENGTH) are reported by the keeping call. Each kind needs a
+ * workspace of its own (gkv_decode_workspace_bytes). */
+typedef enum { GKV_PLAN_NONE = 0, GKV_PLAN_KEEP = 1, GKV_PLAN_REUSE = 2 } gkv_plan_mode;
+int gkv_decode_layer_planned(void *stream, int32_t B, int32_t n_q_heads, const float *qkv,
+                             int64_t row_stride, const float *cos_tab, const float *sin_tab,
+                             const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,
+                             int32_t window, const float *sinks, int32_t split_tokens,
+                             void *workspace, size_t workspace_bytes, void *out,
+                             int64_t out_stride, int32_t out_dtype, uint32_t *dev_err,
+                             int32_t plan);
+/* Its first launch alone, as gkv_decode_layer_split is gkv_decode_layer's
+ * (gkv_decode_combine with the same arguments completes it). */
+int gkv_decode_layer_split_planned(void *stream, int32_t B, int32_t n_q_heads, const float *qkv,
+                                   int64_t row_stride, const float *cos_tab,
+                                   const float *sin_tab, const int32_t *seq_lens,
+                                   int32_t max_seq_len, gkv_cache_view cache, int32_t window,
+                                   const float *sinks, int32_t split_tokens, void *workspace,
+                                   size_t workspace_bytes, void *out, int64_t out_stride,
+                                   int32_t out_dtype, uint32_t *dev_err, int32_t plan);
 
 /* gkv_decode_layer without a workspace argument and without allocating: the
  * workspace is the library's own device array (one per GPU, about 16.5 MiB,

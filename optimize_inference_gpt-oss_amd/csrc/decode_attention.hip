@@ -86,6 +86,14 @@ constexpr int kPrepThreads = 1024;
 constexpr int kMaxBatch = 8192;        // sequences per call (prefix sums kept in LDS)
 constexpr int kBadBlock = -1;          // F entry: id outside the pool
 constexpr int kPadBlock = -2;          // F entry: no tokens (padding)
+// A decode layer's plan kept for the following layers of its kind (the same
+// lengths and table): a key naming what it was built for, then each range's
+// bounds, first sequence and count of sequences; the block ids and step
+// records stay in the range slabs (flat, steps).
+constexpr int kKeyInts = 16;
+constexpr int kPlanMagic = 0x504c4e31;
+constexpr int kKeepPlan = 2;           // fused launch mode bits (bit 0: append)
+constexpr int kReusePlan = 4;
 
 // Step record: sequence << 8 | first step of the sequence << 7 | its last
 // step << 6 | tokens of the step that exist (0..32).
@@ -115,6 +123,7 @@ struct DecodeArgs {
                       // [range][kIdSlab], block k of range w at w * kIdSlab + k
   int32_t *steps;     // step record of every 32-token step: [range][kInfoSlab]
   u32x4 *qops;        // [B][Hkv][64 lanes][2]: query operands
+  int32_t *kept;      // kept plan: [kKeyInts] key, then int4 {rs, re, b_first, n_seq} per range
   float *ws_o;        // [range][kPartsPerRange][Hkv][8][64]: partial outputs
   float *ws_ml;       // [range][kPartsPerRange][Hkv][8][2]: their (m, l)
   void *out;
@@ -298,6 +307,8 @@ __device__ __forceinline__ void prep_blocks(const DecodeArgs &a, int wg, int n_w
       a.plan[1] = S;
       a.plan[2] = min(a.n_wg, (T + S - 1) / S);
       a.plan[3] = 0;
+      if (a.kept)
+        a.kept[0] = 0; // a kept plan is valid until a launch plans afresh
     }
   }
 
@@ -809,6 +820,36 @@ void decode_split_kernel(DecodeArgs a) {
 
 constexpr int kStepsPerThread = kInfoSlab / 64; // record-building steps per thread (>= 64 threads)
 
+// Tokens of a sequence of length L in the stream: its length, or the window,
+// clamped to what the table row and the launch were sized for.
+__device__ __forceinline__ int stream_tokens(const DecodeArgs &a, int L) {
+  const int n = a.window > 0 ? min(L, a.window) : L;
+  return max(min(n, min(a.table_stride * kBlockTokens, a.max_len)), 0);
+}
+
+// Word i of a kept plan's key: what the plan depends on besides the contents
+// of the lengths and of the table.
+__device__ __forceinline__ int plan_key(const DecodeArgs &a, int i) {
+  const uint64_t lens = (uint64_t)(uintptr_t)a.seq_lens, tab = (uint64_t)(uintptr_t)a.table;
+  switch (i) {
+  case 0: return kPlanMagic;
+  case 1: return a.B;
+  case 2: return a.n_wg;
+  case 3: return a.window;
+  case 4: return a.fixed_S;
+  case 5: return a.aligned;
+  case 6: return a.max_len;
+  case 7: return a.table_stride;
+  case 8: return a.num_blocks;
+  case 9: return a.n_kv_heads;
+  case 10: return (int)(uint32_t)lens;
+  case 11: return (int)(uint32_t)(lens >> 32);
+  case 12: return (int)(uint32_t)tab;
+  case 13: return (int)(uint32_t)(tab >> 32);
+  default: return 0;
+  }
+}
+
 // One launch per decode layer before the combine. Every workgroup repeats the
 // plan: the prefix sums of the padded lengths, in LDS (the lengths are 4
 // bytes per sequence). It then builds the step records and block ids of its
@@ -819,9 +860,15 @@ constexpr int kStepsPerThread = kInfoSlab / 64; // record-building steps per thr
 // reads the new tokens back; no other workgroup reads them (each step of the
 // stream belongs to one range). Workgroup 0 publishes the plan for the
 // combine.
+// mode: bit 0 append; kKeepPlan: also keep the plan in the workspace (each
+// range's bounds, block ids and step records, under a key); kReusePlan: take
+// the kept plan instead of planning, when its key matches this launch (else
+// plan afresh and report GKV_DEVERR_PLAN). Layers of one kind in one decode
+// step share the lengths and the table, so one keeps and the others reuse;
+// the ranges, and so every output bit, are the same either way.
 template <int R, int VF>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(1)))
-void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
+void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
   __shared__ int s_cu[kMaxBatch + 1];
   __shared__ int s_len[kMaxBatch];
   __shared__ int2 s_ids[kIdSlab / 2];
@@ -831,121 +878,189 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nt = blockDim.x, B = a.B;
   const int n_waves = nt >> 6;
   const int w_id = blockIdx.x;
+  const bool append = mode & 1, keep = mode & kKeepPlan;
+  int4 *kept_ranges = (int4 *)(a.kept + kKeyInts);
 
-  // Lengths and padded lengths into LDS (coalesced loads), then the prefix
-  // sums in place: thread t scans sequences t*per .. t*per+per-1.
-  bool any_over = false;
-  for (int b = t; b < B; b += nt) {
-    const int L = a.seq_lens[b];
-    int n = a.window > 0 ? min(L, a.window) : L;
-    const int cap = min(a.table_stride * kBlockTokens, a.max_len);
-    any_over |= n > cap;
-    n = max(min(n, cap), 0);
-    s_len[b] = L;
-    s_cu[b] = pad_step(n);
-  }
-  __syncthreads();
-  const int per = (B + nt - 1) / nt;
-  const int b0 = min(t * per, B), b1 = min(b0 + per, B);
-  int local = 0;
-  for (int b = b0; b < b1; b++)
-    local += s_cu[b];
-  int incl = local;
+  bool reuse = false;
+  if (mode & kReusePlan) {
+    bool same = true;
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int v = __shfl_up(incl, off, 64);
-    if (lane >= off)
-      incl += v;
+    for (int i = 0; i < kKeyInts; i++)
+      same &= a.kept[i] == plan_key(a, i);
+    reuse = uniform(same);
+    if (!reuse && w_id == 0 && t == 0 && a.dev_err)
+      atomicOr(a.dev_err, GKV_DEVERR_PLAN);
   }
-  if (lane == 63)
-    s_wave[wave] = incl;
-  __syncthreads();
-  int before = 0, total = 0;
-  for (int w = 0; w < n_waves; w++) {
-    const int v = s_wave[w];
-    before += w < wave ? v : 0;
-    total += v;
-  }
-  int run = before + incl - local;
-  for (int b = b0; b < b1; b++) {
-    const int v = s_cu[b];
-    s_cu[b] = run;
-    run += v;
-  }
-  if (t == 0)
-    s_cu[B] = total;
-  __syncthreads();
-  const int T = s_cu[B];
-  const int S = a.fixed_S > 0 ? a.fixed_S : max(kStep, pad_step((T + a.n_wg - 1) / a.n_wg));
-  if (w_id == 0) {
-    int32_t *cu = a.plan + kPlanHeader;
-    for (int b = t; b <= B; b += nt)
-      cu[b] = s_cu[b];
-    if (t == 0) {
-      a.plan[0] = T;
-      a.plan[1] = S;
-      a.plan[2] = min(a.n_wg, (T + S - 1) / S);
-      a.plan[3] = a.aligned;
+
+  int rs, re, b_first = 0, n_seq = 0;
+  if (reuse) {
+    const int4 h = kept_ranges[w_id];
+    rs = h.x;
+    re = h.y;
+    b_first = h.z;
+    n_seq = h.w;
+    if (a.aligned) {
+      // sequences without tokens: output 0, written by workgroup b % n_wg
+      const int n_out = a.n_kv_heads * a.G * kHeadDim;
+      for (int k = wave * 64; (int64_t)k * a.n_wg + w_id < B; k += nt) {
+        const int b = w_id + (k + lane) * a.n_wg;
+        const bool empty = b < B && stream_tokens(a, a.seq_lens[b]) == 0;
+        uint64_t m = __ballot(empty);
+        while (m) {
+          const int be = w_id + (k + __builtin_ctzll(m)) * a.n_wg;
+          m &= m - 1;
+          for (int i = lane; i < n_out; i += 64)
+            store_out(a.out, (int64_t)be * a.out_stride + i, 0.0f, a.out_bf16);
+        }
+      }
     }
-    if (any_over && a.dev_err)
-      atomicOr(a.dev_err, GKV_DEVERR_LENGTH);
-  }
-  int rs, re;
-  if (a.aligned) {
-    // Ranges of whole sequences, so every segment is a whole sequence,
-    // finished here, and no partial is written. Two cuts, both keeping the
-    // sequences in order: by count, range k holds sequences ceil(k B / n_wg)
-    // .. ceil((k + 1) B / n_wg) - 1 (even when most sequences fill the
-    // window, where a cut by tokens can hand a range a third sequence); by
-    // tokens, range k runs from the first sequence that starts at or after
-    // k T / n_wg (even when the lengths vary below the window). The cut by
-    // count is taken when its longest range is within half a window of the
-    // mean; every workgroup finds the same. Sequences without tokens (output
-    // 0, all weight on the sink) are written by workgroup b % n_wg.
-    auto first_by_count = [&](int k) -> int {
-      return (int)(((int64_t)k * B + a.n_wg - 1) / a.n_wg);
-    };
-    auto start_by_tokens = [&](int k) -> int {
-      if (k >= a.n_wg)
-        return T;
-      const int target = (int)(((int64_t)k * T + a.n_wg - 1) / a.n_wg);
-      int lo = 0, hi = B; // the first i with s_cu[i] >= target (s_cu[B] = T)
+    if (rs >= re)
+      return;
+  } else {
+    // Lengths and padded lengths into LDS (coalesced loads), then the prefix
+    // sums in place: thread t scans sequences t*per .. t*per+per-1.
+    bool any_over = false;
+    for (int b = t; b < B; b += nt) {
+      const int L = a.seq_lens[b];
+      int n = a.window > 0 ? min(L, a.window) : L;
+      const int cap = min(a.table_stride * kBlockTokens, a.max_len);
+      any_over |= n > cap;
+      n = max(min(n, cap), 0);
+      s_len[b] = L;
+      s_cu[b] = pad_step(n);
+    }
+    __syncthreads();
+    const int per = (B + nt - 1) / nt;
+    const int b0 = min(t * per, B), b1 = min(b0 + per, B);
+    int local = 0;
+    for (int b = b0; b < b1; b++)
+      local += s_cu[b];
+    int incl = local;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int v = __shfl_up(incl, off, 64);
+      if (lane >= off)
+        incl += v;
+    }
+    if (lane == 63)
+      s_wave[wave] = incl;
+    __syncthreads();
+    int before = 0, total = 0;
+    for (int w = 0; w < n_waves; w++) {
+      const int v = s_wave[w];
+      before += w < wave ? v : 0;
+      total += v;
+    }
+    int run = before + incl - local;
+    for (int b = b0; b < b1; b++) {
+      const int v = s_cu[b];
+      s_cu[b] = run;
+      run += v;
+    }
+    if (t == 0)
+      s_cu[B] = total;
+    __syncthreads();
+    const int T = s_cu[B];
+    const int S = a.fixed_S > 0 ? a.fixed_S : max(kStep, pad_step((T + a.n_wg - 1) / a.n_wg));
+    if (w_id == 0) {
+      int32_t *cu = a.plan + kPlanHeader;
+      for (int b = t; b <= B; b += nt)
+        cu[b] = s_cu[b];
+      if (t == 0) {
+        a.plan[0] = T;
+        a.plan[1] = S;
+        a.plan[2] = min(a.n_wg, (T + S - 1) / S);
+        a.plan[3] = a.aligned;
+      }
+      // a kept plan is valid until a launch plans afresh on this workspace
+      if (a.kept) {
+        if (keep && t < kKeyInts)
+          a.kept[t] = plan_key(a, t);
+        else if (!keep && t == 0)
+          a.kept[0] = 0;
+      }
+      if (any_over && a.dev_err)
+        atomicOr(a.dev_err, GKV_DEVERR_LENGTH);
+    }
+    if (a.aligned) {
+      // Ranges of whole sequences, so every segment is a whole sequence,
+      // finished here, and no partial is written. Two cuts, both keeping the
+      // sequences in order: by count, range k holds sequences ceil(k B / n_wg)
+      // .. ceil((k + 1) B / n_wg) - 1 (even when most sequences fill the
+      // window, where a cut by tokens can hand a range a third sequence); by
+      // tokens, range k runs from the first sequence that starts at or after
+      // k T / n_wg (even when the lengths vary below the window). The cut by
+      // count is taken when its longest range is within half a window of the
+      // mean; every workgroup finds the same. Sequences without tokens (output
+      // 0, all weight on the sink) are written by workgroup b % n_wg.
+      auto first_by_count = [&](int k) -> int {
+        return (int)(((int64_t)k * B + a.n_wg - 1) / a.n_wg);
+      };
+      auto start_by_tokens = [&](int k) -> int {
+        if (k >= a.n_wg)
+          return T;
+        const int target = (int)(((int64_t)k * T + a.n_wg - 1) / a.n_wg);
+        int lo = 0, hi = B; // the first i with s_cu[i] >= target (s_cu[B] = T)
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (s_cu[mid] >= target)
+            hi = mid;
+          else
+            lo = mid + 1;
+        }
+        return s_cu[lo];
+      };
+      int longest = 0;
+      for (int k = t; k < a.n_wg; k += nt)
+        longest = max(longest, s_cu[first_by_count(k + 1)] - s_cu[first_by_count(k)]);
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1)
+        longest = max(longest, __shfl_xor(longest, off));
+      if (lane == 0)
+        s_max[wave] = longest;
+      __syncthreads();
+      for (int w = 0; w < n_waves; w++)
+        longest = max(longest, s_max[w]);
+      const bool by_count = longest <= (T + a.n_wg - 1) / a.n_wg + a.window / 2 &&
+                            longest <= kMaxRange;
+      rs = by_count ? s_cu[first_by_count(w_id)] : start_by_tokens(w_id);
+      re = by_count ? s_cu[first_by_count(w_id + 1)] : start_by_tokens(w_id + 1);
+      const int n_out = a.n_kv_heads * a.G * kHeadDim;
+      for (int b = w_id; b < B; b += a.n_wg)
+        if (s_cu[b + 1] == s_cu[b])
+          for (int i = t; i < n_out; i += nt)
+            store_out(a.out, (int64_t)b * a.out_stride + i, 0.0f, a.out_bf16);
+    } else {
+      rs = min(w_id * S, T);
+      re = min(rs + S, T);
+    }
+    // The sequences that overlap the range, a run of consecutive indices:
+    // from the one holding position rs (the last b with cu[b] <= rs) to the
+    // last one starting before re.
+    if (rs < re && (append || keep)) {
+      int lo = 0, hi = B - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_cu[mid] <= rs)
+          lo = mid;
+        else
+          hi = mid - 1;
+      }
+      b_first = lo;
+      hi = B; // the first b with cu[b] >= re (cu[B] = T >= re)
       while (lo < hi) {
         const int mid = (lo + hi) >> 1;
-        if (s_cu[mid] >= target)
+        if (s_cu[mid] >= re)
           hi = mid;
         else
           lo = mid + 1;
       }
-      return s_cu[lo];
-    };
-    int longest = 0;
-    for (int k = t; k < a.n_wg; k += nt)
-      longest = max(longest, s_cu[first_by_count(k + 1)] - s_cu[first_by_count(k)]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-      longest = max(longest, __shfl_xor(longest, off));
-    if (lane == 0)
-      s_max[wave] = longest;
-    __syncthreads();
-    for (int w = 0; w < n_waves; w++)
-      longest = max(longest, s_max[w]);
-    const bool by_count = longest <= (T + a.n_wg - 1) / a.n_wg + a.window / 2 &&
-                          longest <= kMaxRange;
-    rs = by_count ? s_cu[first_by_count(w_id)] : start_by_tokens(w_id);
-    re = by_count ? s_cu[first_by_count(w_id + 1)] : start_by_tokens(w_id + 1);
-    const int n_out = a.n_kv_heads * a.G * kHeadDim;
-    for (int b = w_id; b < B; b += a.n_wg)
-      if (s_cu[b + 1] == s_cu[b])
-        for (int i = t; i < n_out; i += nt)
-          store_out(a.out, (int64_t)b * a.out_stride + i, 0.0f, a.out_bf16);
+      n_seq = lo - b_first;
+    }
+    if (keep && t == 0)
+      kept_ranges[w_id] = int4{rs, max(re, rs), b_first, n_seq};
     if (rs >= re)
       return;
-  } else {
-    rs = w_id * S;
-    if (rs >= T)
-      return;
-    re = min(rs + S, T);
   }
   // The range is the same for every lane; saying so keeps the stream's
   // addresses in scalar registers (a bound the compiler takes for divergent,
@@ -953,71 +1068,79 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
   // stream a loop over lanes).
   rs = uniform(rs);
   re = uniform(re);
+  b_first = uniform(b_first);
+  n_seq = uniform(n_seq);
   const int n_steps = (re - rs) / kStep;
 
-  // The new tokens in the range: the sequences that overlap it are a run of
-  // consecutive indices, each checked for its new token's place in the
-  // stream (its last position, or its ring slot). Wave w appends candidates
-  // w, w + 4, ...; the loads of its first go out now, before the step records'
-  // table loads, and it finishes after them.
-  int b_first = 0;
-  if (append) {
-    int lo = 0, hi = B - 1; // the sequence holding position rs: last b with cu[b] <= rs
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_cu[mid] <= rs)
-        lo = mid;
-      else
-        hi = mid - 1;
-    }
-    b_first = lo;
-  }
+  // The new tokens in the range: each sequence that overlaps it is checked
+  // for its new token's place in the stream (its last position, or its ring
+  // slot). Wave w appends candidates w, w + 4, ...; the loads of its first go
+  // out now, before the step records' loads, and it finishes after them.
+  const int32_t *plan_cu = a.plan + kPlanHeader;
+  auto cu_of = [&](int b) -> int { return reuse ? plan_cu[b] : s_cu[b]; };
+  auto len_of = [&](int b) -> int { return reuse ? a.seq_lens[b] : s_len[b]; };
   auto new_token_in_range = [&](int b) -> bool {
-    const int L = s_len[b];
-    int n = a.window > 0 ? min(L, a.window) : L;
-    n = max(min(n, min(a.table_stride * kBlockTokens, a.max_len)), 0);
+    const int L = len_of(b);
     const int slot = a.window > 0 ? (L - 1) % a.window : L - 1;
-    const int at = s_cu[b] + slot;
-    return L >= 1 && slot < n && at >= rs && at < re;
+    const int at = cu_of(b) + slot;
+    return L >= 1 && slot < stream_tokens(a, L) && at >= rs && at < re;
   };
   AppendLoads first_row;
   int first_b = -1;
-  if (append) {
+  if (append && wave < n_seq) {
     const int b = b_first + wave;
-    if (b < B && s_cu[b] < re && new_token_in_range(b)) {
-      first_row = append_begin(ap, b, lane, s_len[b] - 1);
+    if (new_token_in_range(b)) {
+      first_row = append_begin(ap, b, lane, len_of(b) - 1);
       first_b = b;
     }
   }
 
-  // Step records and block ids of the range (the table loads go out here).
+  // Step records and block ids of the range (the table loads, or the kept
+  // slabs' loads, go out here).
   int id0[kStepsPerThread], id1[kStepsPerThread], rcd[kStepsPerThread];
+  if (reuse) {
+    const int2 *src = (const int2 *)(a.flat + (int64_t)w_id * kIdSlab);
+    const int *srec = a.steps + (int64_t)w_id * kInfoSlab;
 #pragma unroll
-  for (int k = 0; k < kStepsPerThread; k++) {
-    const int i = t + k * nt;
-    id0[k] = id1[k] = kPadBlock;
-    rcd[k] = 0;
-    if (i < n_steps) {
-      const int tok = rs + i * kStep;
-      int lo = 0, hi = B - 1; // the sequence holding the step: last b with cu[b] <= tok
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (s_cu[mid] <= tok)
-          lo = mid;
-        else
-          hi = mid - 1;
+    for (int k = 0; k < kStepsPerThread; k++) {
+      const int i = t + k * nt;
+      id0[k] = id1[k] = kPadBlock;
+      rcd[k] = 0;
+      if (i < n_steps) {
+        const int2 p = src[i];
+        id0[k] = p.x;
+        id1[k] = p.y;
+        rcd[k] = srec[i];
       }
-      const int b = lo;
-      const int off = tok - s_cu[b];
-      const int L = s_len[b];
-      int n = a.window > 0 ? min(L, a.window) : L;
-      n = max(min(n, min(a.table_stride * kBlockTokens, a.max_len)), 0);
-      const int32_t *row = a.table + (int64_t)b * a.table_stride + off / kBlockTokens;
-      if (off < n)
-        id0[k] = row[0];
-      if (off + kBlockTokens < n)
-        id1[k] = row[1];
-      rcd[k] = step_record(b, off == 0, tok + kStep == s_cu[b + 1], min(max(n - off, 0), kStep));
+    }
+    for (int j = t; j < n_seq; j += nt)
+      s_len[b_first + j] = a.seq_lens[b_first + j];
+  } else {
+#pragma unroll
+    for (int k = 0; k < kStepsPerThread; k++) {
+      const int i = t + k * nt;
+      id0[k] = id1[k] = kPadBlock;
+      rcd[k] = 0;
+      if (i < n_steps) {
+        const int tok = rs + i * kStep;
+        int lo = 0, hi = B - 1; // the sequence holding the step: last b with cu[b] <= tok
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (s_cu[mid] <= tok)
+            lo = mid;
+          else
+            hi = mid - 1;
+        }
+        const int b = lo;
+        const int off = tok - s_cu[b];
+        const int n = stream_tokens(a, s_len[b]);
+        const int32_t *row = a.table + (int64_t)b * a.table_stride + off / kBlockTokens;
+        if (off < n)
+          id0[k] = row[0];
+        if (off + kBlockTokens < n)
+          id1[k] = row[1];
+        rcd[k] = step_record(b, off == 0, tok + kStep == s_cu[b + 1], min(max(n - off, 0), kStep));
+      }
     }
   }
 
@@ -1025,12 +1148,10 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
   if (first_b >= 0)
     append_end(ap, first_row, first_b, lane);
   if (append) {
-    for (int j = wave + n_waves;; j += n_waves) {
+    for (int j = wave + n_waves; j < n_seq; j += n_waves) {
       const int b = b_first + j;
-      if (b >= B || s_cu[b] >= re)
-        break;
       if (new_token_in_range(b))
-        append_row(ap, b, lane, 0, 1, nullptr, s_len[b] - 1);
+        append_row(ap, b, lane, 0, 1, nullptr, len_of(b) - 1);
     }
   }
 
@@ -1050,6 +1171,10 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int append) {
       }
       s_ids[i] = int2{x, y};
       s_rec[i] = rcd[k];
+      if (keep) {
+        ((int2 *)(a.flat + (int64_t)w_id * kIdSlab))[i] = int2{x, y};
+        a.steps[(int64_t)w_id * kInfoSlab + i] = rcd[k];
+      }
     }
   }
   if (any_bad && a.dev_err)
@@ -1188,10 +1313,11 @@ static int resident_workgroups(int n_kv_heads) {
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Workspace layout: plan | partials (o) | partials (m, l) | then, for the
-// staged launches only: block ids | step records | query operands. The split
-// that plans in its prologue uses the first three (fused_total bytes).
+// staged launches and the kept plan only: block ids | step records | query
+// operands | kept plan. The split that plans in its prologue uses the first
+// three (fused_total bytes).
 struct WorkspaceLayout {
-  size_t plan, ws_o, ws_ml, flat, steps, qops, fused_total, total;
+  size_t plan, ws_o, ws_ml, flat, steps, qops, kept, fused_total, total;
 };
 
 static WorkspaceLayout layout_of(int B, int n_kv_heads, int max_wg) {
@@ -1204,7 +1330,8 @@ static WorkspaceLayout layout_of(int B, int n_kv_heads, int max_wg) {
   L.fused_total = L.flat;
   L.steps = L.flat + align256((size_t)max_wg * kIdSlab * 4);
   L.qops = L.steps + align256((size_t)max_wg * kInfoSlab * 4);
-  L.total = L.qops + align256((size_t)B * n_kv_heads * 64 * 32);
+  L.kept = L.qops + align256((size_t)B * n_kv_heads * 64 * 32);
+  L.total = L.kept + align256((size_t)(kKeyInts + 4 * max_wg) * 4);
   return L;
 }
 
@@ -1316,6 +1443,7 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
   a.flat = (int32_t *)(ws + L.flat);
   a.steps = (int32_t *)(ws + L.steps);
   a.qops = (u32x4 *)(ws + L.qops);
+  a.kept = staged_parts ? (int32_t *)(ws + L.kept) : nullptr;
   a.ws_o = (float *)(ws + L.ws_o);
   a.ws_ml = (float *)(ws + L.ws_ml);
   a.out = out;
@@ -1370,34 +1498,36 @@ static int launch_split(const DecodeArgs &a, hipStream_t s) {
 }
 
 template <int R>
-static void launch_fused_ring(const DecodeArgs &a, const AppendArgs &ap, int append, dim3 grid,
+static void launch_fused_ring(const DecodeArgs &a, const AppendArgs &ap, int mode, dim3 grid,
                               dim3 block, hipStream_t s) {
   if (a.kv_fp8)
-    hipLaunchKernelGGL((decode_fused_kernel<R, 2>), grid, block, 0, s, a, ap, append);
+    hipLaunchKernelGGL((decode_fused_kernel<R, 2>), grid, block, 0, s, a, ap, mode);
   else if (a.vs)
-    hipLaunchKernelGGL((decode_fused_kernel<R, 1>), grid, block, 0, s, a, ap, append);
+    hipLaunchKernelGGL((decode_fused_kernel<R, 1>), grid, block, 0, s, a, ap, mode);
   else
-    hipLaunchKernelGGL((decode_fused_kernel<R, 0>), grid, block, 0, s, a, ap, append);
+    hipLaunchKernelGGL((decode_fused_kernel<R, 0>), grid, block, 0, s, a, ap, mode);
 }
 
-// The fused launch; ap == nullptr: no append (attention only).
-static int launch_fused(const DecodeArgs &a, const AppendArgs *ap, hipStream_t s) {
+// The fused launch; ap == nullptr: no append (attention only). plan_bits:
+// kKeepPlan / kReusePlan (a workspace with the kept-plan area).
+static int launch_fused(const DecodeArgs &a, const AppendArgs *ap, hipStream_t s,
+                        int plan_bits = 0) {
   const dim3 grid(a.n_wg), block(split_block(a.n_kv_heads));
   AppendArgs aa{};
   if (ap) {
     aa = *ap;
     aa.seq_lens = nullptr; // the kernel passes each row's position (its length - 1)
   }
-  const int append = ap ? 1 : 0;
+  const int mode = (ap ? 1 : 0) | plan_bits;
   switch (ring_depth()) {
   case 3:
-    launch_fused_ring<3>(a, aa, append, grid, block, s);
+    launch_fused_ring<3>(a, aa, mode, grid, block, s);
     break;
   case 5:
-    launch_fused_ring<5>(a, aa, append, grid, block, s);
+    launch_fused_ring<5>(a, aa, mode, grid, block, s);
     break;
   default:
-    launch_fused_ring<4>(a, aa, append, grid, block, s);
+    launch_fused_ring<4>(a, aa, mode, grid, block, s);
   }
   return launch_status("decode_fused_kernel");
 }
@@ -1563,6 +1693,26 @@ extern "C" int gkv_decode_layer(GKV_LAYER_PARAMS) {
   if ((st = launch_fused(a, &ap, (hipStream_t)stream)))
     return st;
   return a.aligned ? GKV_OK : launch_combine(a, (hipStream_t)stream);
+}
+
+static int plan_bits(int32_t plan) {
+  return plan == GKV_PLAN_KEEP ? kKeepPlan : plan == GKV_PLAN_REUSE ? kReusePlan : 0;
+}
+
+extern "C" int gkv_decode_layer_planned(GKV_LAYER_PARAMS, int32_t plan) {
+  if (plan != GKV_PLAN_NONE && plan != GKV_PLAN_KEEP && plan != GKV_PLAN_REUSE)
+    return GKV_ERR_ARG;
+  GKV_LAYER_SETUP
+  if ((st = launch_fused(a, &ap, (hipStream_t)stream, plan_bits(plan))))
+    return st;
+  return a.aligned ? GKV_OK : launch_combine(a, (hipStream_t)stream);
+}
+
+extern "C" int gkv_decode_layer_split_planned(GKV_LAYER_PARAMS, int32_t plan) {
+  if (plan != GKV_PLAN_NONE && plan != GKV_PLAN_KEEP && plan != GKV_PLAN_REUSE)
+    return GKV_ERR_ARG;
+  GKV_LAYER_SETUP
+  return launch_fused(a, &ap, (hipStream_t)stream, plan_bits(plan));
 }
 
 

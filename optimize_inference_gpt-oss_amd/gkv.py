@@ -101,6 +101,12 @@ SIGNATURES = {
     "gkv_decode_layer": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
                                         CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
                                         _vp]),
+    "gkv_decode_layer_planned": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
+                                        CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
+                                        _vp, _i32]),
+    "gkv_decode_layer_split_planned": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp,
+                                              _vp, _i32, CacheView, _i32, _vp, _i32, _vp, _sz,
+                                              _vp, _i64, _i32, _vp, _i32]),
     "gkv_decode_layer_noalloc": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
                                                CacheView, _i32, _vp, _vp, _i64, _i32, _vp]),
     "gkv_decode_layer_split": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
@@ -302,6 +308,28 @@ def decode_layer(qkv, seq_lens, max_seq_len, view: CacheView, sinks, out, cos_ta
     decode_attention(qkv, seq_lens, max_seq_len, view, sinks, out, window=window,
                      cos_tab=cos_tab, sin_tab=sin_tab, split_tokens=split_tokens,
                      workspace=workspace, dev_err=dev_err, stream=stream, stage="layer")
+
+
+PLAN_NONE, PLAN_KEEP, PLAN_REUSE = 0, 1, 2
+DEVERR_PLAN = 16
+
+
+def decode_layer_planned(qkv, seq_lens, max_seq_len, view: CacheView, sinks, out, cos_tab,
+                         sin_tab, plan, window=0, split_tokens=0, workspace=None, dev_err=None,
+                         stream=None, split_only=False):
+    """gkv_decode_layer_planned: gkv_decode_layer that keeps (PLAN_KEEP) or reuses
+    (PLAN_REUSE) the split launch's plan in the workspace. split_only: the
+    first launch alone (gkv_decode_layer_split_planned)."""
+    import torch
+    out_dtype = BF16 if out.dtype == torch.bfloat16 else F32
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    name = "gkv_decode_layer_split_planned" if split_only else "gkv_decode_layer_planned"
+    st = getattr(lib(), name)(stream_handle(stream), qkv.shape[0], sinks.shape[0], ptr(qkv),
+                              qkv.stride(0), ptr(cos_tab), ptr(sin_tab), ptr(seq_lens),
+                              max_seq_len, view, window, ptr(sinks), split_tokens,
+                              ptr(workspace), ws_bytes, ptr(out), out.stride(0), out_dtype,
+                              ptr(dev_err), plan)
+    check(name, st)
 
 
 def decode_layer_noalloc(qkv, seq_lens, max_seq_len, view: CacheView, sinks, out, cos_tab,

@@ -146,6 +146,23 @@ def test_decode_argument_checks(gkv):
     assert call(B=4, max_len=1 << 20, split=32, ws=fake, ws_bytes=need) == gkv.GKV_ERR_ARG
 
 
+def test_planned_layer_argument_checks(gkv):
+    """gkv_decode_layer_planned takes the modes 0-2 only; otherwise it checks
+    as gkv_decode_layer does (B = 0: nothing to do)."""
+    L = gkv.lib()
+    fake = 0x1000  # never dereferenced: the checks fail first
+    need = gkv.workspace_bytes(4, 8, 100)
+    def call(plan, B=4, ws_bytes=need):
+        return L.gkv_decode_layer_planned(None, B, 64, fake, 80 * 64, fake, fake, fake, 100,
+                                          _view(gkv), 0, fake, 0, fake, ws_bytes, fake, 4096,
+                                          0, None, plan)
+    assert call(3) == gkv.GKV_ERR_ARG
+    assert call(-1) == gkv.GKV_ERR_ARG
+    for plan in (gkv.PLAN_NONE, gkv.PLAN_KEEP, gkv.PLAN_REUSE):
+        assert call(plan, ws_bytes=need - 1) == gkv.GKV_ERR_WORKSPACE
+        assert call(plan, B=0) == gkv.GKV_OK
+
+
 def test_fp8_cache_where_unsupported(gkv):
     """The prefill over a history rejects the e4m3 cache; the appends need its
     scales."""
@@ -180,14 +197,16 @@ def test_workspace_formula(gkv):
     # up to 1024 ranges, 8 heads x (64 + 2) floats per kv head; then, for the
     # staged launches, block ids (1024 per range) and step records (512 per
     # range: ranges of up to 16384 tokens) and the query operands (2 KB per
-    # sequence and kv head); each part 256-byte aligned
+    # sequence and kv head), then the kept plan (a 16-int key and 4 ints per
+    # range); each part 256-byte aligned
     def a256(x):
         return (x + 255) // 256 * 256
 
     B, hkv = 512, 8
     parts = 2 * 1024 * hkv
     fused = a256(a256((4 + B + 1) * 4) + parts * (512 + 16) * 4)
-    staged = a256(1024 * 1024 * 4) + a256(1024 * 512 * 4) + a256(B * hkv * 2048)
+    staged = (a256(1024 * 1024 * 4) + a256(1024 * 512 * 4) + a256(B * hkv * 2048)
+              + a256((16 + 4 * 1024) * 4))
     assert gkv.workspace_bytes(B, hkv, 2049) == fused + staged
     # a window layer bounds the stream by the window
     assert gkv.workspace_bytes(B, hkv, 100000, window=128) == gkv.workspace_bytes(B, hkv, 128)
