@@ -103,13 +103,21 @@ inline void attention_bf16_chunk64(stream_t s, const float *qkv, int row_stride,
 // layer) or attention_bf16_chunk64 (bf16 V), the pair at gpu_engine.hpp:495-498,
 // as one gkv_decode_layer call (the append runs in the attention's launch).
 // Row b is the new token at row_pos[b]; the output is bf16.
+// plan: the engine's loop over layers (gpu_engine.hpp:652) can pass
+// GKV_PLAN_KEEP for the first layer of each kind (full, window) in a step and
+// GKV_PLAN_REUSE for the others of that kind, each kind with a workspace of its
+// own (workspace: nullptr = bt.workspace; the same size), so that the later
+// layers skip the planning (gkv_decode_layer_planned; the same output bits).
 inline void rope_kv_attention_bf16(stream_t s, int B, const float *qkv, int row_stride,
                                    const PagedLayer &layer, int n_q_heads, bf16_t *out,
-                                   int out_stride, const PagedBatch &bt) {
-  check(gkv_decode_layer(s, B, n_q_heads, qkv, row_stride, bt.cos_tab, bt.sin_tab,
-                         bt.seq_lens, bt.max_seq_len, layer.view, layer.window, layer.sinks, 0,
-                         bt.workspace, bt.workspace_bytes, out, out_stride, GKV_BF16,
-                         bt.dev_err),
+                                   int out_stride, const PagedBatch &bt,
+                                   gkv_plan_mode plan = GKV_PLAN_NONE,
+                                   void *workspace = nullptr) {
+  check(gkv_decode_layer_planned(s, B, n_q_heads, qkv, row_stride, bt.cos_tab, bt.sin_tab,
+                                 bt.seq_lens, bt.max_seq_len, layer.view, layer.window,
+                                 layer.sinks, 0, workspace ? workspace : bt.workspace,
+                                 bt.workspace_bytes, out, out_stride, GKV_BF16, bt.dev_err,
+                                 plan),
         "rope_kv_attention_bf16");
 }
 

@@ -5,8 +5,11 @@
 // tables, then per layer rope_kv_bf16(rotate_q = false) and
 // attention_bf16_chunk64 with the query rotated on load.
 //
-//   gkv_engine_demo <in.bin> <out.bin> [fused | project | q8v]
+//   gkv_engine_demo <in.bin> <out.bin> [fused | planned | project | q8v]
 // fused: the one-call form rope_kv_attention_bf16 instead of the two calls.
+// planned: rope_kv_attention_bf16 with the plan kept by the first layer of
+//   each kind (full, window) in a step and reused by the others, a workspace
+//   per kind.
 // q8v: the engine's own fast-path pair, rope_kv_bf16 + attention_q8v_chunk64
 //   (gpu_engine.hpp:495-498; the pool must hold the int8-V cache).
 // project: the qkv rows come from the layer input through the QKV projection
@@ -47,6 +50,7 @@ int main(int argc, char **argv) {
   const bool fused = argc == 4 && std::string(argv[3]) == "fused";
   const bool project = argc == 4 && std::string(argv[3]) == "project";
   const bool q8v = argc == 4 && std::string(argv[3]) == "q8v";
+  const bool planned = argc == 4 && std::string(argv[3]) == "planned";
   FILE *f = fopen(argv[1], "rb");
   if (!f)
     return 2;
@@ -103,7 +107,7 @@ int main(int argc, char **argv) {
   uint32_t *d_err;
   uint16_t *d_out;
   const size_t ws_bytes = gkv_decode_workspace_bytes(B, Hkv, P, 0, 0);
-  void *d_ws;
+  void *d_ws, *d_ws_window;
   HIP_OK(hipMalloc(&d_qkv, (size_t)B * QKV * 4));
   HIP_OK(hipMalloc(&d_sinks, sinks.size() * 4));
   HIP_OK(hipMalloc(&d_cos, cos_h.size() * 4));
@@ -113,6 +117,7 @@ int main(int argc, char **argv) {
   HIP_OK(hipMalloc(&d_err, 4));
   HIP_OK(hipMalloc(&d_out, (size_t)B * ATT * 2));
   HIP_OK(hipMalloc(&d_ws, ws_bytes));
+  HIP_OK(hipMalloc(&d_ws_window, ws_bytes));
   uint16_t *d_x = nullptr, *d_w = nullptr;
   float *d_b = nullptr;
   if (project) {
@@ -158,6 +163,12 @@ int main(int argc, char **argv) {
                               (size_t)B * QKV * 4, hipMemcpyHostToDevice, s));
         if (fused) {
           gkv_engine::rope_kv_attention_bf16(s, B, d_qkv, QKV, layers[l], Hq, d_out, ATT, bt);
+        } else if (planned) {
+          const bool window_kind = layers[l].window > 0;
+          const bool first_of_kind = l < 2 && (l == 0 || window_kind != (layers[0].window > 0));
+          gkv_engine::rope_kv_attention_bf16(s, B, d_qkv, QKV, layers[l], Hq, d_out, ATT, bt,
+                                             first_of_kind ? GKV_PLAN_KEEP : GKV_PLAN_REUSE,
+                                             window_kind ? d_ws_window : d_ws);
         } else if (q8v) {
           // layer_attention's lines, the cache arguments replaced by the paged layer
           gkv_engine::rope_kv_bf16(s, B, d_qkv, QKV, bt, Hq, layers[l], /*rotate_q=*/false);
@@ -185,7 +196,8 @@ int main(int argc, char **argv) {
   fclose(g);
   gkv_pool_destroy(pool);
   for (void *ptr : {(void *)d_qkv, (void *)d_sinks, (void *)d_cos, (void *)d_sin, (void *)d_pos,
-                    (void *)d_lens, (void *)d_err, (void *)d_out, d_ws, (void *)d_x, (void *)d_w,
+                    (void *)d_lens, (void *)d_err, (void *)d_out, d_ws, d_ws_window, (void *)d_x,
+                    (void *)d_w,
                     (void *)d_b})
     (void)hipFree(ptr);
   (void)hipStreamDestroy(s);

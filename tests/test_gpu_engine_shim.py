@@ -28,16 +28,19 @@ def _bf16_values(a):
 
 
 @pytest.mark.parametrize("mode,v_int8", [(None, False), ("fused", False), ("fused", True),
-                                         ("project", False), ("q8v", True)])
+                                         ("planned", False), ("project", False),
+                                         ("q8v", True)])
 def test_engine_shim_decode_loop(oracle, cuda, tmp_path, mode, v_int8):
     """mode None: rope_kv_bf16 + attention_bf16_chunk64; "q8v": rope_kv_bf16 +
     attention_q8v_chunk64 in the reference's argument order; "fused": the one-call
-    rope_kv_attention_bf16; "project": the qkv rows come from the layer input
+    rope_kv_attention_bf16; "planned": the same over four layers, the first of
+    each kind keeping its plan and the others reusing it; "project": the qkv
+    rows come from the layer input
     through gemm_bf16_rope_kv (projection with the append in its epilogue),
     and the oracle's rows from orc_linear (run.cpp matmul + bias)."""
     if not os.path.exists(DEMO):
         pytest.fail("gkv_engine_demo is not built (run __graft_entry__.build())")
-    P, B, Hq, Hkv, NL, W = 40, 3, 64, 8, 2, 32
+    P, B, Hq, Hkv, NL, W = 40, 3, 64, 8, 4 if mode == "planned" else 2, 32
     rng = np.random.default_rng(2024)
     QKV = (Hq + 2 * Hkv) * 64
     qkv = (rng.standard_normal((P, NL, B, QKV)) * 0.5).astype(np.float32)
