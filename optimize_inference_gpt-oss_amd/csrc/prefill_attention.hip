@@ -300,57 +300,45 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   };
 
   // ---- query operands: column tile c holds queries q0 + 16c + n; half dh dims 32dh + 8kg + j.
-  // The loads of both column tiles (and of their RoPE angles) and of the
-  // first K/V tile go out together: one memory round trip before compute.
+  // The loads of both column tiles, of the block's RoPE angles and of the
+  // first K/V tiles go out together: one memory round trip before compute.
+  // The angles (cos and sin of the block's 32 positions, [2][32][32] fp32, 8
+  // KB) are the same for every wave: they are staged once per workgroup, one
+  // 1 KB direct-to-LDS load per wave (8 positions of cos or of sin), into the
+  // second V^T buffer, which the first tile's conversion of the next one
+  // overwrites only after its barrier. (Loaded by every wave into registers
+  // they cost each workgroup 32 KB of cache traffic and its last waves 1.4 us
+  // of start.) The rotation and the bf16 split follow the first barrier.
   // the block ids of the first tiles go out first
   const Ids ids0 = load_ids(0), ids1 = load_ids(1);
   Ids ids_next = load_ids(kStages - 1);
+  const bool rot = a.cos_tab != nullptr;
+  float *const ang = (float *)(v_lds + D * kVRow);
   bf16x8 qhi[2][2], qlo[2][2];
+  f32x4 qr[2][4];
   {
-    const float qscale = 0.125f * kLog2e; // 1/sqrt(64); exp -> exp2
-    const bool rot = a.cos_tab != nullptr;
-    f32x4 qr[2][4], cr[2][2], sr[2][2];
 #pragma unroll
     for (int c = 0; c < 2; c++) {
-      const int j = min(q0 + 16 * c + n, L - 1), pos = start + j;
+      const int j = min(q0 + 16 * c + n, L - 1);
       const float *qp = a.q + (int64_t)(row0 + j) * a.q_stride + h * D + 8 * kg;
       // the two halves of RoPE pairs 8kg .. 8kg+7 sit in this lane
       qr[c][0] = *(const f32x4 *)qp;
       qr[c][1] = *(const f32x4 *)(qp + 4);
       qr[c][2] = *(const f32x4 *)(qp + 32);
       qr[c][3] = *(const f32x4 *)(qp + 36);
-      // without RoPE the angle loads re-read the query (any valid address)
-      const float *cp = rot ? a.cos_tab + (int64_t)pos * (D / 2) + 8 * kg : qp;
-      const float *sp = rot ? a.sin_tab + (int64_t)pos * (D / 2) + 8 * kg : qp;
-      cr[c][0] = *(const f32x4 *)cp;
-      cr[c][1] = *(const f32x4 *)(cp + 4);
-      sr[c][0] = *(const f32x4 *)sp;
-      sr[c][1] = *(const f32x4 *)(sp + 4);
+    }
+    if (rot) {
+#pragma unroll
+      for (int k = wave; k < 8; k += NW) {
+        const int i = 8 * (k & 3) + (lane >> 3); // the position's row in the block
+        const float *tab = k < 4 ? a.cos_tab : a.sin_tab;
+        dma16(tab + (int64_t)(start + min(q0 + i, L - 1)) * (D / 2) + 4 * (lane & 7),
+              ang + k * 256);
+      }
     }
 #pragma unroll
     for (int t = 0; t < kStages - 1; t++)
       dma(t, t, t == 0 ? ids0 : ids1);
-#pragma unroll
-    for (int c = 0; c < 2; c++) {
-      float qv[2][8];
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const float x1 = qr[c][j / 4][j % 4], x2 = qr[c][2 + j / 4][j % 4];
-        const float cs = cr[c][j / 4][j % 4], sn = sr[c][j / 4][j % 4];
-        qv[0][j] = rot ? rope_first(x1, x2, cs, sn) : x1;
-        qv[1][j] = rot ? rope_second(x1, x2, cs, sn) : x2;
-      }
-#pragma unroll
-      for (int dh = 0; dh < 2; dh++) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const float x = qv[dh][j] * qscale;
-          const __bf16 hi = (__bf16)x;
-          qhi[c][dh][j] = hi;
-          qlo[c][dh][j] = (__bf16)(x - (float)hi);
-        }
-      }
-    }
   }
   const float sink2 = a.sinks[h] * kLog2e;
   float m_run[2] = {sink2, sink2}, lsum[2] = {0.0f, 0.0f};
@@ -475,9 +463,41 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
     if (HIST)
       ids_next = load_ids(t + kStages);
   };
-  // tile 0's V^T before the loop (tile 1's loads may still fly)
+  // the query (rotated, scaled, split), then tile 0's V^T, before the loop
+  // (tile 1's loads may still fly)
   wait_vmcnt<2 * (8 / NW)>();
   lds_barrier();
+  {
+    const float qscale = 0.125f * kLog2e; // 1/sqrt(64); exp -> exp2
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+      f32x4 cr[2] = {}, sr[2] = {};
+      if (rot) {
+        const float *cp = ang + (16 * c + n) * (D / 2) + 8 * kg;
+        cr[0] = *(const f32x4 *)cp;
+        cr[1] = *(const f32x4 *)(cp + 4);
+        sr[0] = *(const f32x4 *)(cp + 1024);
+        sr[1] = *(const f32x4 *)(cp + 1028);
+      }
+      float qv[2][8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const float x1 = qr[c][j / 4][j % 4], x2 = qr[c][2 + j / 4][j % 4];
+        qv[0][j] = rot ? rope_first(x1, x2, cr[j / 4][j % 4], sr[j / 4][j % 4]) : x1;
+        qv[1][j] = rot ? rope_second(x1, x2, cr[j / 4][j % 4], sr[j / 4][j % 4]) : x2;
+      }
+#pragma unroll
+      for (int dh = 0; dh < 2; dh++) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const float x = qv[dh][j] * qscale;
+          const __bf16 hi = (__bf16)x;
+          qhi[c][dh][j] = hi;
+          qlo[c][dh][j] = (__bf16)(x - (float)hi);
+        }
+      }
+    }
+  }
   convert_v(0, 0, 0);
   for (int t = 0; t < n_tiles; t += kStages) {
     tile(t, 0);
