@@ -18,7 +18,8 @@ INT8_POISON = 0x55  # codes of int8-V slots that hold no token
 
 
 def v_int8_offsets(t):
-    """Byte offsets of dims 0..63 of token t (0..15) in a head's 1 KB int8 V block."""
+    """Byte offsets of dims 0..63 of token t (0..15) in a head's 1 KB int8 V block
+    (t an int, or an array [..., 1] for one row of offsets per token)."""
     d = np.arange(D)
     return ((d % 16) * 4 + t // 4) * 16 + (d // 16) * 4 + t % 4
 
@@ -43,7 +44,8 @@ def v_block_offsets():
 
 def k_fp8_offsets(t):
     """Byte offsets of dims 0..63 of token t in a head's 1 KB e4m3 K block: lane
-    kg*16 + t loads 16 bytes at lane*16, dims 8kg..8kg+7 then 32+8kg..+7."""
+    kg*16 + t loads 16 bytes at lane*16, dims 8kg..8kg+7 then 32+8kg..+7 (t an
+    int, or an array [..., 1])."""
     d = np.arange(D)
     return ((d % 32) // 8 * 16 + t) * 16 + (d // 32) * 8 + d % 8
 
@@ -192,24 +194,27 @@ class DecodeCase:
         phys = self.table[b, slots // BT]
         k[phys, :, slots % BT, :] = kh
 
+    def _slots(self, b, slots):
+        """Physical block [n, 1, 1], token in block [n] and head index [1, Hkv, 1]
+        of the listed slots of sequence b."""
+        slots = np.asarray(slots)
+        phys = self.table[b, slots // BT].astype(np.int64)[:, None, None]
+        return phys, slots % BT, np.arange(self.Hkv)[None, :, None]
+
     def _place_v8(self, v, vs, b, slots, codes, scales):
         """codes [n, Hkv, 64] int8, scales [n, Hkv] -> the int8 block layout."""
-        for j, slot in enumerate(np.asarray(slots)):
-            phys = self.table[b, slot // BT]
-            t = int(slot % BT)
-            v[phys][:, v_int8_offsets(t)] = codes[j]
-            vs[phys, :, t] = scales[j]
+        phys, t, g = self._slots(b, slots)
+        v[phys, g, v_int8_offsets(t[:, None])[:, None, :]] = codes
+        vs[phys[:, 0, 0], :, t] = scales
 
     def _place_f8(self, k, v, s, b, slots, kcodes, kscales, vcodes, vscales):
         """e4m3 codes [n, Hkv, 64] and scales [n, Hkv] -> the e4m3 block layouts,
         K scales at token t, V scales at 16 + t."""
-        for j, slot in enumerate(np.asarray(slots)):
-            phys = self.table[b, slot // BT]
-            t = int(slot % BT)
-            k[phys][:, k_fp8_offsets(t)] = kcodes[j]
-            v[phys][:, v_int8_offsets(t)] = vcodes[j]
-            s[phys, :, t] = kscales[j]
-            s[phys, :, BT + t] = vscales[j]
+        phys, t, g = self._slots(b, slots)
+        k[phys, g, k_fp8_offsets(t[:, None])[:, None, :]] = kcodes
+        v[phys, g, v_int8_offsets(t[:, None])[:, None, :]] = vcodes
+        s[phys[:, 0, 0], :, t] = kscales
+        s[phys[:, 0, 0], :, BT + t] = vscales
 
     def _place(self, b, slots, kh, vh):
         phys = self.table[b, slots // BT]
