@@ -219,3 +219,44 @@ def test_empty_batch_and_zero_length(oracle, gkv, cuda):
     gkv.prefill_attention(z, 0, q, kv, kv, torch.zeros(64, device=cuda), out, 8)
     torch.cuda.synchronize()
     assert float(out.abs().sum()) == 0.0
+
+
+def _sweep_draw(seed):
+    rng = np.random.default_rng(9100 + seed)
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    G = int(rng.choice([1, 2, 3, 4, 6, 8]))
+    B = int(rng.integers(1, 25))
+    kind = str(rng.choice(["short", "mixed", "long"]))
+    if kind == "short":
+        L = rng.integers(0, 48, size=B)
+    elif kind == "mixed":
+        L = np.where(rng.random(B) < 0.15, 0, rng.integers(1, 600, size=B))
+    else:
+        L = rng.integers(300, 900, size=B)
+    # at most ~4000 prompt rows, so the oracle finishes in seconds
+    L = L[:max(1, int(np.searchsorted(np.cumsum(L), 4000)))]
+    window = int(rng.choice([0, 0, 16, 32, 128]))
+    return dict(Hq=Hkv * G, Hkv=Hkv, L=L, window=window, rot=bool(rng.random() < 0.5),
+                bf16=bool(rng.random() < 0.3), scale=float(rng.choice([0.5, 1.0, 2.0])),
+                seed=9200 + seed)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_prefill_sweep(oracle, gkv, cuda, seed):
+    """Seeded shapes: kv heads 1-8, 1-8 query heads per kv head, 1-24 prompts
+    of 0 to 900 tokens, windows 0/16/32/128, Q rotated by the append or on
+    load, fp32 or bf16 output, value scales 0.5-2. The append is bit-exact
+    (rotated Q when the append writes it, packed rows, cache bytes) and the
+    output within max-abs 2e-3 + rel 1e-2 (plus bf16 rounding)."""
+    import torch
+    p = _sweep_draw(seed)
+    print(f"prefill sweep {seed}: Hq={p['Hq']} Hkv={p['Hkv']} B={len(p['L'])} "
+          f"rows={int(p['L'].sum())} W={p['window']} rot={p['rot']} bf16={p['bf16']}",
+          flush=True)
+    case = PrefillCase(oracle, p["seed"], p["L"], p["Hq"], p["Hkv"], window=p["window"],
+                       scale=p["scale"])
+    res = run_gpu(case, gkv, torch, cuda, out_dtype=torch.bfloat16 if p["bf16"] else None,
+                  rotate_in_prefill=p["rot"])
+    if p["rot"]:
+        res["q"] = case.q_rot  # the append wrote no rotated Q
+    check(case, res, rtol=RTOL + (2.0 ** -8 if p["bf16"] else 0.0))
