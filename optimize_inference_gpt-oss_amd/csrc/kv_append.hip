@@ -38,7 +38,12 @@ __global__ __launch_bounds__(64 * kRowsPerWg) void kv_append_kernel(AppendArgs a
   const int r = blockIdx.x * kRowsPerWg + w;
   const bool staged = !a.v_int8 && !a.kv_fp8 && a.vc && a.n_kv_heads <= kMaxStageHeads;
   RowPlace pl{0, -1, -1, 0};
-  if (r < n_rows)
+  // Without a rotated-query output the row's loads go out at once (its K or
+  // V pieces, then its place and angles) and the stores follow; else the
+  // general form.
+  if (r < n_rows && !a.q_out && a.n_kv_heads <= 8)
+    pl = append_end(a, append_begin(a, r, lane, -1), r, lane, staged ? s_v[w] : nullptr);
+  else if (r < n_rows)
     pl = append_row(a, r, lane, 0, 1, staged ? s_v[w] : nullptr);
   if (!staged)
     return;

@@ -284,10 +284,12 @@ __device__ __forceinline__ RowPlace append_row(const AppendArgs &a, int r, int l
 }
 
 // A row's append in two halves, for a caller that overlaps the row's loads
-// with other work: append_begin issues the loads (the placement's table
-// entry, the lane's K or V pieces, the angles), append_end rotates, rounds and
-// stores, as append_row does. One wave per row, at most 8 kv heads, no
-// rotated-query output; the caller knows the row's position.
+// with other work: append_begin issues the loads (the lane's K or V pieces
+// first, as they depend on the row only; then the placement's table entry
+// and the angles), append_end rotates, rounds and stores, as append_row does.
+// One wave per row, at most 8 kv heads, no rotated-query output. pos: the
+// row's position if the caller knows it, else -1 (row_pos[r], or the last
+// position of its sequence).
 struct AppendLoads {
   int seq, slot, off, table_entry; // table_entry: the block id as loaded (-1: none)
   bool store;
@@ -299,16 +301,6 @@ __device__ __forceinline__ AppendLoads append_begin(const AppendArgs &a, int r, 
                                                     int pos) {
   constexpr int D = kHeadDim, HALF = kHeadDim / 2;
   AppendLoads L;
-  L.seq = a.row_seq ? a.row_seq[r] : r;
-  L.slot = a.ring > 0 ? pos % a.ring : pos;
-  L.off = L.slot % kBlockTokens;
-  L.store = a.kc != nullptr;
-  if (L.store && a.ring > 0 && a.seq_lens && pos + a.ring < a.seq_lens[L.seq])
-    L.store = false; // a later row of this call takes the ring slot
-  const int blk = L.slot / kBlockTokens;
-  L.table_entry = L.store && blk < a.table_stride
-                      ? a.table[(int64_t)L.seq * a.table_stride + blk]
-                      : -1;
   // The same four loads on every lane (no divergent branch, so the loaded
   // registers are not merged through memory): a key lane's dims 8j..+7 and
   // 32+8j..+7, a value lane's 16q..16q+15; lanes past the heads re-read the
@@ -323,6 +315,18 @@ __device__ __forceinline__ AppendLoads append_begin(const AppendArgs &a, int r, 
   L.x[1] = *(const f32x4 *)(xp + 4);
   L.x[2] = *(const f32x4 *)(xp + second);
   L.x[3] = *(const f32x4 *)(xp + second + 4);
+  L.seq = a.row_seq ? a.row_seq[r] : r;
+  if (pos < 0)
+    pos = a.row_pos ? a.row_pos[r] : a.seq_lens[L.seq] - 1;
+  L.slot = a.ring > 0 ? pos % a.ring : pos;
+  L.off = L.slot % kBlockTokens;
+  L.store = a.kc != nullptr;
+  if (L.store && a.ring > 0 && a.seq_lens && pos + a.ring < a.seq_lens[L.seq])
+    L.store = false; // a later row of this call takes the ring slot
+  const int blk = L.slot / kBlockTokens;
+  L.table_entry = L.store && blk < a.table_stride
+                      ? a.table[(int64_t)L.seq * a.table_stride + blk]
+                      : -1;
   const float *cp = a.cos_tab + (int64_t)pos * HALF + 8 * j;
   const float *sp = a.sin_tab + (int64_t)pos * HALF + 8 * j;
   L.cs[0] = *(const f32x4 *)cp;
@@ -332,8 +336,8 @@ __device__ __forceinline__ AppendLoads append_begin(const AppendArgs &a, int r, 
   return L;
 }
 
-__device__ __forceinline__ void append_end(const AppendArgs &a, const AppendLoads &L, int r,
-                                           int lane) {
+__device__ __forceinline__ RowPlace append_end(const AppendArgs &a, const AppendLoads &L,
+                                               int r, int lane, uint16_t *v_stage = nullptr) {
   constexpr int D = kHeadDim;
   bool store = L.store;
   int64_t base = 0;
@@ -350,16 +354,18 @@ __device__ __forceinline__ void append_end(const AppendArgs &a, const AppendLoad
       base = (int64_t)L.table_entry * a.n_kv_heads * (kBlockTokens * D);
     }
   }
+  const RowPlace place{store ? 1 : 0, L.seq, L.slot, base};
   const int g = (lane & 31) / 4, j = lane % 4;
   if (g >= a.n_kv_heads)
-    return;
+    return place;
   if (lane < 32) {
     const f32x4 x1[2] = {L.x[0], L.x[1]}, x2[2] = {L.x[2], L.x[3]};
     const f32x4 c[2] = {L.cs[0], L.cs[1]}, s[2] = {L.cs[2], L.cs[3]};
     append_keys(a, r, g, j, x1, x2, c, s, store, base, L.off);
   } else {
-    append_values(a, r, g, j, L.x, store, base, L.off, nullptr);
+    append_values(a, r, g, j, L.x, store, base, L.off, v_stage);
   }
+  return place;
 }
 
 } // namespace gkv
