@@ -5,7 +5,7 @@
 A step is one pass of the hot path over the batch: KV append (RoPE on K, bf16
 store into the paged cache) plus split-K GQA flash-decoding attention (split
 and combine kernels) of one layer, for every sequence of the batch. Default
-workload: BASELINE config 2, the gpt-oss-20b-shape full-attention decode layer
+workload: config 2, the gpt-oss-20b-shape full-attention decode layer
 (B=512, H_q=64, H_kv=8, d=64, bf16 paged cache of 16-token blocks with a
 randomly permuted block table, context lengths U[128, 2048], values
 N(0,1)*0.5, sinks N(0,1)). Config 3 is the 128-token sliding-window layer

@@ -1,4 +1,4 @@
-"""Full-size decode layers on a gkv pool, for GPU tests at BASELINE batch sizes.
+"""Full-size decode layers on a gkv pool, for GPU tests at the benchmark configs' batch sizes.
 
 The cache history is random bf16 written on the device (the host never holds
 the whole cache). What the tests check:

@@ -3,7 +3,7 @@
 Appends are compared bit for bit (every byte of the paged cache, including the
 NaN-poisoned slots that must stay untouched); attention outputs within
 max-abs 2e-3 + rel 1e-2 (bf16 cache, fp32 accumulate), the tolerance of the
-north-star contract. Inputs are seeded; shapes follow the BASELINE configs
+north-star contract. Inputs are seeded; shapes follow the benchmark configs
 (reduced batch where the CPU oracle has to run the whole batch).
 """
 import numpy as np
