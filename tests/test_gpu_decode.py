@@ -174,6 +174,17 @@ def test_edge_lengths(gkv, cuda, torch_mod):
     check_case(case, run_gpu(case, gkv, torch_mod, cuda))
 
 
+@pytest.mark.parametrize("split_tokens", [0, 16384])
+def test_long_sequences(gkv, cuda, torch_mod, split_tokens):
+    """Contexts far past one range: 40k and 20k tokens beside short ones. With
+    the balanced split a 40k context spans over a hundred ranges, all merged
+    by the combine; with 16384-token ranges (the largest a range holds) the
+    ranges' block ids and step records fill their LDS slabs."""
+    L = np.array([40000, 5, 20000, 16391], np.int32)
+    case = DecodeCase(len(L), 64, 8, L, window=0, scale=0.5, seed=57)
+    check_case(case, run_gpu(case, gkv, torch_mod, cuda, split_tokens=split_tokens))
+
+
 @pytest.mark.parametrize("split_tokens", [128, 256, 512, 1024])
 def test_split_sizes_agree(gkv, cuda, torch_mod, split_tokens):
     L = np.array([5, 300, 700, 1300, 2047], np.int32)
