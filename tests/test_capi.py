@@ -130,6 +130,7 @@ def test_decode_argument_checks(gkv):
     assert call(lens=None) == gkv.GKV_ERR_ARG
     assert call(hq=128 + 8) == gkv.GKV_ERR_UNSUPPORTED          # 17 query heads per kv head
     assert call(split=100) == gkv.GKV_ERR_ARG                   # not a multiple of 128
+    assert call(B=8193) == gkv.GKV_ERR_UNSUPPORTED             # more sequences than one call takes
     assert call(out_stride=100) == gkv.GKV_ERR_ARG
     assert call(dtype=7) == gkv.GKV_ERR_ARG
     assert call(view=_view(gkv, ring=128), window=0) == gkv.GKV_ERR_ARG

@@ -185,6 +185,16 @@ def test_long_sequences(gkv, cuda, torch_mod, split_tokens):
     check_case(case, run_gpu(case, gkv, torch_mod, cuda, split_tokens=split_tokens))
 
 
+@pytest.mark.parametrize("window", [0, 32])
+def test_largest_batch(gkv, cuda, torch_mod, window):
+    """8192 sequences, the most one call takes (the split's prefix sums and
+    lengths sit in LDS), short contexts, through gkv_decode_layer."""
+    rng = np.random.default_rng(58 + window)
+    L = lens_uniform(rng, 8192, 0, 48)
+    case = DecodeCase(len(L), 64, 8, L, window=window, scale=0.5, seed=59)
+    check_case(case, run_gpu(case, gkv, torch_mod, cuda, layer_call=True))
+
+
 @pytest.mark.parametrize("split_tokens", [128, 256, 512, 1024])
 def test_split_sizes_agree(gkv, cuda, torch_mod, split_tokens):
     L = np.array([5, 300, 700, 1300, 2047], np.int32)
