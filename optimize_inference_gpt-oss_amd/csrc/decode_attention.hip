@@ -118,7 +118,7 @@ struct DecodeArgs {
   int n_wg;           // split workgroups launched
   int fixed_S;        // 0: S = T / n_wg (balanced); > 0: this S
   int aligned;        // ranges of whole sequences (fused launch only; no partials)
-  int32_t *plan;      // [kPlanHeader][cu: B + 1]
+  int32_t *plan;      // [kPlanHeader][cu: B + 1][boundary sequence: one per range]
   int32_t *flat;      // block id of every 16-token block of the stream, per range:
                       // [range][kIdSlab], block k of range w at w * kIdSlab + k
   int32_t *steps;     // step record of every 32-token step: [range][kInfoSlab]
@@ -310,6 +310,31 @@ __device__ __forceinline__ void prep_blocks(const DecodeArgs &a, int wg, int n_w
       if (a.kept)
         a.kept[0] = 0; // a kept plan is valid until a launch plans afresh
     }
+    // per range, the sequence it starts inside of (-1: none), for the combine
+    for (int w = t; w < a.n_wg; w += kPrepThreads) {
+      const int tok = w * S;
+      int v = -1;
+      if (tok < T) {
+        int lo = 0, hi = B - 1; // the last b with cu[b] <= tok
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (s_cu[mid] <= tok)
+            lo = mid;
+          else
+            hi = mid - 1;
+        }
+        v = tok > s_cu[lo] ? lo : -1;
+      }
+      a.plan[kPlanHeader + B + 1 + w] = v;
+    }
+  }
+  // sequences without tokens: output 0
+  {
+    const int n_out = a.n_kv_heads * a.G * kHeadDim;
+    for (int b = wg; b < B; b += n_wgs)
+      if (s_cu[b + 1] == s_cu[b])
+        for (int i = t; i < n_out; i += kPrepThreads)
+          store_out(a.out, (int64_t)b * a.out_stride + i, 0.0f, a.out_bf16);
   }
 
   // Stream blocks (and the step records at even blocks), grid-strided.
@@ -899,7 +924,7 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
     re = h.y;
     b_first = h.z;
     n_seq = h.w;
-    if (a.aligned) {
+    {
       // sequences without tokens: output 0, written by workgroup b % n_wg
       const int n_out = a.n_kv_heads * a.G * kHeadDim;
       for (int k = wave * 64; (int64_t)k * a.n_wg + w_id < B; k += nt) {
@@ -1037,7 +1062,7 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
     // The sequences that overlap the range, a run of consecutive indices:
     // from the one holding position rs (the last b with cu[b] <= rs) to the
     // last one starting before re.
-    if (rs < re && (append || keep)) {
+    if (rs < re) {
       int lo = 0, hi = B - 1;
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -1059,6 +1084,18 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
     }
     if (keep && t == 0)
       kept_ranges[w_id] = int4{rs, max(re, rs), b_first, n_seq};
+    if (!a.aligned) {
+      // The sequence this range starts inside of (-1: none), for the combine
+      // launched per range boundary; and the sequences without tokens
+      // (output 0), written by workgroup b % n_wg.
+      if (t == 0)
+        a.plan[kPlanHeader + B + 1 + w_id] = rs < re && rs > s_cu[b_first] ? b_first : -1;
+      const int n_out = a.n_kv_heads * a.G * kHeadDim;
+      for (int b = w_id; b < B; b += a.n_wg)
+        if (s_cu[b + 1] == s_cu[b])
+          for (int i = t; i < n_out; i += nt)
+            store_out(a.out, (int64_t)b * a.out_stride + i, 0.0f, a.out_bf16);
+    }
     if (rs >= re)
       return;
   }
@@ -1199,19 +1236,17 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
 
 // ---- combine --------------------------------------------------------------------
 
-// One workgroup per sequence, wave g for kv head g; lane (h = lane / 8) merges
-// dims 8*(lane % 8) .. +7 of query head h over the sequence's partials:
+// Sequence b's output from its partials, one wave per kv head g; lane (h =
+// lane / 8) merges dims 8*(lane % 8) .. +7 of query head h over them:
 // M = max(sink, m_w), L = 2^(sink-M) + sum l_w 2^(m_w-M), out = sum o_w 2^(m_w-M) / L
-// (the merge of fast_attention.hpp:403-424, across workgroups).
-__global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
+// (the merge of fast_attention.hpp:403-424, across workgroups). Returns at
+// once if the sequence lies in one range (finished by its split workgroup).
+__device__ __forceinline__ void combine_sequence(const DecodeArgs &a, int b) {
   constexpr int D = kHeadDim;
-  const int b = blockIdx.x;
   const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, h = lane >> 3, d0 = 8 * (lane & 7);
   if (h >= a.G)
     return;
-  if (a.plan[3])
-    return; // whole-sequence ranges: the split launch finished every sequence
   const int32_t *cu = a.plan + kPlanHeader;
   const int S = a.plan[1];
   const int c0 = cu[b], c1 = cu[b + 1];
@@ -1250,6 +1285,22 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
     store_out(a.out, ob + i, o0[i] * inv, a.out_bf16);
     store_out(a.out, ob + 4 + i, o1[i] * inv, a.out_bf16);
   }
+}
+
+// One workgroup per range: the split launches (or the prepare launch of the
+// staged ones) have written the outputs of sequences without tokens and, per
+// range, the sequence the range starts inside of; range w merges that
+// sequence unless an earlier range starts inside it too. n_wg workgroups
+// instead of one per sequence, most of them returning at once.
+__global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
+  if (a.plan[3])
+    return;
+  const int w = blockIdx.x;
+  const int32_t *bnd = a.plan + kPlanHeader + a.B + 1;
+  const int b = bnd[w];
+  if (b < 0 || (w > 0 && bnd[w - 1] == b))
+    return;
+  combine_sequence(a, b);
 }
 
 // ---- host side --------------------------------------------------------------------
@@ -1323,7 +1374,7 @@ struct WorkspaceLayout {
 static WorkspaceLayout layout_of(int B, int n_kv_heads, int max_wg) {
   WorkspaceLayout L;
   L.plan = 0;
-  L.ws_o = align256((size_t)(kPlanHeader + B + 1) * 4);
+  L.ws_o = align256((size_t)(kPlanHeader + B + 1 + max_wg) * 4);
   const size_t parts = (size_t)kPartsPerRange * max_wg * n_kv_heads;
   L.ws_ml = L.ws_o + parts * kPartFloats * sizeof(float);
   L.flat = align256(L.ws_ml + parts * kMlStride * sizeof(float));
@@ -1408,7 +1459,8 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
   if (!workspace || workspace_bytes_given < (staged_parts ? L.total : L.fused_total))
     return GKV_ERR_WORKSPACE;
   if (split_tokens == 0) {
-    const int resident = (need_cache && B > 0) ? resident_workgroups(cache.n_kv_heads) : 1;
+    // (the combine takes the same count: one workgroup per range)
+    const int resident = B > 0 ? resident_workgroups(cache.n_kv_heads) : 1;
     if (resident <= 0)
       return GKV_ERR_HIP;
     n_wg = std::max<int64_t>(resident, min_wg);
@@ -1533,7 +1585,7 @@ static int launch_fused(const DecodeArgs &a, const AppendArgs *ap, hipStream_t s
 }
 
 static int launch_combine(const DecodeArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(a.B), dim3(64 * a.n_kv_heads), 0, s, a);
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(a.n_wg), dim3(64 * a.n_kv_heads), 0, s, a);
   return launch_status("decode_combine_kernel");
 }
 
@@ -1730,7 +1782,7 @@ extern "C" int gkv_decode_layer_split_planned(GKV_LAYER_PARAMS, int32_t plan) {
 namespace gkv {
 constexpr int kScratchWorkgroups = 512; // ranges (split workgroups) the scratch holds
 constexpr size_t kScratchBytes =
-    ((((size_t)(kPlanHeader + kMaxBatch + 1) * 4 + 255) & ~(size_t)255) +
+    ((((size_t)(kPlanHeader + kMaxBatch + 1 + kScratchWorkgroups) * 4 + 255) & ~(size_t)255) +
      (size_t)kPartsPerRange * kScratchWorkgroups * 8 * (kPartFloats + kMlStride) * 4 + 255) &
     ~(size_t)255;
 static __device__ __align__(256) char scratch[kScratchBytes];

@@ -194,7 +194,7 @@ def test_layer_combines_argument_checks(gkv):
 
 
 def test_workspace_formula(gkv):
-    # plan (header + prefix sums); partial results of 2 segments per range for
+    # plan (header + prefix sums + one boundary sequence per range); partial results of 2 segments per range for
     # up to 1024 ranges, 8 heads x (64 + 2) floats per kv head; then, for the
     # staged launches, block ids (1024 per range) and step records (512 per
     # range: ranges of up to 16384 tokens) and the query operands (2 KB per
@@ -205,7 +205,7 @@ def test_workspace_formula(gkv):
 
     B, hkv = 512, 8
     parts = 2 * 1024 * hkv
-    fused = a256(a256((4 + B + 1) * 4) + parts * (512 + 16) * 4)
+    fused = a256(a256((4 + B + 1 + 1024) * 4) + parts * (512 + 16) * 4)
     staged = (a256(1024 * 1024 * 4) + a256(1024 * 512 * 4) + a256(B * hkv * 2048)
               + a256((16 + 4 * 1024) * 4))
     assert gkv.workspace_bytes(B, hkv, 2049) == fused + staged
