@@ -32,8 +32,10 @@
 //            finished in place (sink added, output written); a piece of a
 //            longer sequence leaves (m, l, o) partials in the workspace at
 //            index b + w (unique: ranges are contiguous).
-//   combine  one workgroup per sequence split over several ranges: merges the
-//            partials with the sink; writes zeros for empty sequences.
+//   combine  one workgroup per range: the range's split launch (or the prep
+//            launch) recorded the sequence the range starts inside of; the
+//            first range inside a sequence merges its partials with the
+//            sink. Empty sequences get zeros from the split (or prep) launch.
 //
 // Matrix cores: v_mfma_f32_16x16x32_bf16, 16x16 output, K = 32.
 //   scores  S^T[token][col] = K[token][dims] * Q^T[dims][col]      (2 MFMAs per 16 tokens)
