@@ -47,8 +47,8 @@
 // XOR-swizzled per key row (conflict-free operand reads without padding);
 // with one, packed K goes into the block layout too (one operand form), V
 // stays in rows. The V of tile t + 1 is turned into V^T [64 dims][64 keys + 8 pad]
-// fp16 while tile t is computed, into the other of two V^T buffers, so a tile
-// needs one barrier.
+// fp16 after tile t is computed, into the other of two V^T buffers: two
+// barriers per tile, and a tile's loads have two tiles' compute to land in.
 #include "gkv_device.hpp"
 #include "lds_dma.hpp"
 
@@ -349,17 +349,17 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
     for (int nn = 0; nn < 4; nn++)
       o[c][nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Tile t in stage st: wait until this wave's loads of tile t + 1 have
-  // landed (issued one tile ago), then the barrier makes every wave's loads
-  // visible, the V^T of tile t (converted during tile t - 1) complete, and
-  // frees the stage of tile t - 1 and the V^T buffer it used: the stage takes
-  // the loads of tile t + kStages - 1, the buffer the V^T of tile t + 1. One
-  // barrier per tile.
+  // Tile t in stage st: the first barrier completes the V^T of tile t
+  // (converted at the end of tile t - 1); the stage of tile t - 1, free since
+  // then, takes the loads of tile t + kStages - 1. After the compute, wait
+  // until this wave's loads of tile t + 1 have landed (issued one tile ago;
+  // those of tile t + 2 stay in flight), and the second barrier makes every
+  // wave's loads visible and frees the V^T buffer of tile t - 1, which takes
+  // the V^T of tile t + 1. A tile's loads thus have two tiles' compute to
+  // land in.
   auto tile = [&](const int t, const int st) {
-    wait_vmcnt<0>();
     lds_barrier();
     dma(t + kStages - 1, (st + kStages - 1) % kStages, ids_next);
-    convert_v((st + 1) % kStages, (t + 1) & 1, t + 1);
     const uint16_t *ks = k_stage(st);
     const uint16_t *vt = v_lds + (t & 1) * (D * kVRow);
     const int kt0 = k_lo + t * kKTile;
@@ -462,6 +462,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
     // the block ids of the tile whose loads the next tile issues
     if (HIST)
       ids_next = load_ids(t + kStages);
+    if (t + 1 < n_tiles) {
+      wait_vmcnt<16 / NW>();
+      lds_barrier();
+      convert_v((st + 1) % kStages, (t + 1) & 1, t + 1);
+    }
   };
   // the query (rotated, scaled, split), then tile 0's V^T, before the loop
   // (tile 1's loads may still fly)
@@ -554,12 +559,12 @@ static void launch_prefill(const gkv::PrefillArgs &a, int G, dim3 g, hipStream_t
     hipLaunchKernelGGL((prefill_kernel<1, HIST>), g, dim3(64), 0, s, a);
 }
 
-// Query blocks per band of the grid order (4, or GKV_PREFILL_BAND, read
+// Query blocks per band of the grid order (2, or GKV_PREFILL_BAND, read
 // once; 1 is the plain longest-first order).
 static int query_band() {
   static const int env = [] {
     const char *e = getenv("GKV_PREFILL_BAND");
-    return e ? std::max(1, atoi(e)) : 4;
+    return e ? std::max(1, atoi(e)) : 2;
   }();
   return env;
 }
