@@ -313,7 +313,8 @@ def run_prefill(torch, gkv, args) -> int:
     row_seq = np.repeat(np.arange(B), L).astype(np.int32)
     need = int(((L + 15) // 16).sum())
     pool = gkv.Pool(n_layers=2, n_kv_heads=Hkv, max_seqs=B, max_seq_len=max_len,
-                    window=cfg["window"], num_blocks=need + 64, shuffle_seed=args.seed)
+                    window=cfg["window"], num_blocks=need + 64, shuffle_seed=args.seed,
+                    v_format=gkv.V_INT8 if args.v_int8 else gkv.V_BF16)
     for b in range(B):
         assert pool.seq_alloc() == b
         if pool.reserve(b, int(L[b])) != 0:
@@ -403,6 +404,8 @@ def run_prefill(torch, gkv, args) -> int:
     alg_bytes = float(T * Hq * D * 4 + T * Hkv * D * 2 * 2 + T * Hq * D * 2)
     achieved = alg_bytes / (dom_ms * 1e-3) / 1e9
     traffic, traffic_note = load_traffic("prefill_config4_traffic")
+    if args.prefill_from_cache or args.v_int8:
+        traffic, traffic_note = None, "the traffic profile covers packed rows and a bf16 cache"
     line = {
         "metric": "causal prefill attention throughput (TFLOP/s), config 4",
         "value": round(sum(fl) / (ms_per_step * 1e-3) / 1e12, 2),
@@ -414,6 +417,8 @@ def run_prefill(torch, gkv, args) -> int:
         "config": {
             "workload": f"config 4: {cfg['name']}", "B": B, "H_q": Hq, "H_kv": Hkv,
             "head_dim": D, "prompt_tokens": T, "lengths": f"U[{cfg['lo']},{cfg['hi']}]",
+            "v_cache": "int8+scale" if args.v_int8 else "bf16",
+            "full_layer_keys": "paged cache" if args.prefill_from_cache else "packed rows",
             "kernel_ms": {("window" if layers[i]["window"] else "full"): {
                 "append": round(float(np.mean([x[0] for x in kern[i]])), 4),
                 "prefill": round(float(np.mean([x[1] for x in kern[i]])), 4)}

@@ -74,6 +74,7 @@ struct PrefillArgs {
   const uint16_t *k, *v;          // packed rows (nullptr: every key from the cache)
   int64_t kv_stride; // elements per packed row: Hkv * 64
   const uint16_t *kc, *vc;        // the paged cache (K and V block layouts)
+  const float *vs;                // int8 V: the cache's V scales, [block][kv head][16]
   const int32_t *table;
   int table_stride, num_blocks, ring;
   const float *sinks;
@@ -87,9 +88,12 @@ struct PrefillArgs {
 
 // HIST: prompts may continue a cached history (start positions, keys from
 // the cache); without it every key comes from the packed rows and the
-// history paths are compiled out.
-template <int NW, bool HIST>
+// history paths are compiled out. V8 (with HIST): the cache's V is int8
+// codes with a scale per token and head; a cached group's V stage then holds
+// the block's 1 KB of codes, then its 16 scales (64 bytes).
+template <int NW, bool HIST, bool V8 = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8 ? 4 : 1))) void prefill_kernel(PrefillArgs a) {
+  static_assert(HIST || !V8, "int8 V comes from the cache");
   constexpr int D = kHeadDim;
   constexpr int NT = NW * 64;
   constexpr int kPieces = kKTile * D / 8 / NT; // V^T conversion: key pairs x 4 dims per thread
@@ -213,7 +217,18 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
         asm volatile("" : "+v"(lane_));
       const uint16_t *src;
       uint32_t off;
-      if (HIST && p < hist_end) {
+      if (V8 && is_v && p < hist_end) {
+        // a cached int8 V block: half 0 its 1 KB of codes, half 1 its 16
+        // scales (lanes 0-3; the other lanes repeat them)
+        const int64_t blk = cached_block(ids, grp); // bf16 elements of a block = int8 bytes
+        if (half) {
+          src = (const uint16_t *)a.vs + blk / 32;
+          off = (lane_ & 3) * 8;
+        } else {
+          src = a.vc + blk / 2;
+          off = lane_ * 8;
+        }
+      } else if (HIST && p < hist_end) {
         // a cached block: its 2 KB as they are (block layouts); tiles past
         // the last re-read the last one
         src = (is_v ? a.vc : a.kc) + cached_block(ids, grp) + half * 512;
@@ -246,10 +261,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   // virtual wave vw = (tid + i*NT) / 64 and its lane ln give
   // pr = ln % 16 + 16 (vw % 2), pd = ln / 16 + 4 (vw / 2); the pair is one
   // dword per dim of V^T, and the 64 dwords a wave writes fall in 64 banks.
-  auto v_half = [](uint32_t bits16) -> uint32_t {
-    const _Float16 h = (_Float16)(bf16_to_f32((uint16_t)bits16) * kVScale);
+  auto f32_half = [](float x) -> uint32_t {
+    const _Float16 h = (_Float16)(x * kVScale);
     return (uint32_t)__builtin_bit_cast(uint16_t, h);
   };
+  auto v_half = [&](uint32_t bits16) -> uint32_t { return f32_half(bf16_to_f32((uint16_t)bits16)); };
   bool v_range = false; // a V beyond the fp16 range of the staged v * 2^-10
   auto convert_v = [&](int st, int buf, int t) {
     const uint16_t *vs = v_stage(st);
@@ -261,38 +277,64 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
       const int vw = idx >> 6, ln = idx & 63;
       const int pr = (ln & 15) + 16 * (vw & 1), pd = (ln >> 4) + 4 * (vw >> 1);
       const int r0 = 2 * pr, r1 = 2 * pr + 1;
-      uint32_t pair[4]; // dims 4pd + j of keys r0 (low half) and r1 (high half)
-      if (HIST && kt0 + (r0 & ~(kBlockTokens - 1)) < hist_end) {
-        // block layout: keys r0, r1 of one dim are adjacent. Slots past the
-        // block's last query position may never have been written: their V
-        // becomes 0 (their weight is 0, and 0 * NaN would not be)
+      // dims 4pd + j of keys r0 (low half) and r1 (high half), as fp16 of v * 2^-10
+      uint32_t hp[4];
+      if (V8 && kt0 + (r0 & ~(kBlockTokens - 1)) < hist_end) {
+        // int8 block: the codes of keys r0, r1 of dim d are adjacent bytes
+        // at ((d % 16) * 4 + t / 4) * 16 + (d / 16) * 4 + t % 4; the value is
+        // code * scale in fp32, as the cache stands for it. Slots past the
+        // block's last query position become 0.
         const uint16_t *blk = vs + (r0 >> 4) * 1024;
+        const float *scl = (const float *)(blk + 512);
         const int t0 = r0 & 15;
-        const uint32_t keep = (kt0 + r0 <= p_last ? 0x0000ffffu : 0u) |
-                              (kt0 + r1 <= p_last ? 0xffff0000u : 0u);
+        const bool keep0 = kt0 + r0 <= p_last, keep1 = kt0 + r1 <= p_last;
+        const float s0 = scl[t0], s1 = scl[t0 + 1];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
           const int d = 4 * pd + j;
-          pair[j] = keep & *(const uint32_t *)(blk + (d >> 5) * 512 +
-                                               ((t0 >> 2) * 16 + (d & 15)) * 8 +
-                                               ((d >> 4) & 1) * 4 + (t0 & 3));
+          const uint32_t c2 = *(const uint16_t *)((const char *)blk +
+                                                  ((d & 15) * 4 + (t0 >> 2)) * 16 +
+                                                  (d >> 4) * 4 + (t0 & 3));
+          const float x0 = keep0 ? (float)(int8_t)(c2 & 0xffu) * s0 : 0.0f;
+          const float x1 = keep1 ? (float)(int8_t)(c2 >> 8) * s1 : 0.0f;
+          hp[j] = f32_half(x0) | (f32_half(x1) << 16);
         }
       } else {
-        const u32x2 x = *(const u32x2 *)(vs + r0 * D + 8 * ((pd >> 1) ^ (r0 & 7)) + 4 * (pd & 1));
-        const u32x2 y = *(const u32x2 *)(vs + r1 * D + 8 * ((pd >> 1) ^ (r1 & 7)) + 4 * (pd & 1));
+        uint32_t pair[4]; // bf16 bits
+        if (HIST && kt0 + (r0 & ~(kBlockTokens - 1)) < hist_end) {
+          // block layout: keys r0, r1 of one dim are adjacent. Slots past the
+          // block's last query position may never have been written: their V
+          // becomes 0 (their weight is 0, and 0 * NaN would not be)
+          const uint16_t *blk = vs + (r0 >> 4) * 1024;
+          const int t0 = r0 & 15;
+          const uint32_t keep = (kt0 + r0 <= p_last ? 0x0000ffffu : 0u) |
+                                (kt0 + r1 <= p_last ? 0xffff0000u : 0u);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const uint32_t wa = x[j >> 1] >> (16 * (j & 1)), wb = y[j >> 1] >> (16 * (j & 1));
-          pair[j] = (wa & 0xffffu) | (wb << 16);
+          for (int j = 0; j < 4; j++) {
+            const int d = 4 * pd + j;
+            pair[j] = keep & *(const uint32_t *)(blk + (d >> 5) * 512 +
+                                                 ((t0 >> 2) * 16 + (d & 15)) * 8 +
+                                                 ((d >> 4) & 1) * 4 + (t0 & 3));
+          }
+        } else {
+          const u32x2 x = *(const u32x2 *)(vs + r0 * D + 8 * ((pd >> 1) ^ (r0 & 7)) + 4 * (pd & 1));
+          const u32x2 y = *(const u32x2 *)(vs + r1 * D + 8 * ((pd >> 1) ^ (r1 & 7)) + 4 * (pd & 1));
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const uint32_t wa = x[j >> 1] >> (16 * (j & 1)), wb = y[j >> 1] >> (16 * (j & 1));
+            pair[j] = (wa & 0xffffu) | (wb << 16);
+          }
         }
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          hp[j] = v_half(pair[j] & 0xffffu) | (v_half(pair[j] >> 16) << 16);
       }
       bool inf = false;
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const uint32_t h0 = v_half(pair[j] & 0xffffu), h1 = v_half(pair[j] >> 16);
         if (HIST) // the entry point with an error word
-          inf |= (h0 & 0x7fffu) == 0x7c00u || (h1 & 0x7fffu) == 0x7c00u;
-        *(uint32_t *)&vt_w[(4 * pd + j) * kVRow + 2 * pr] = h0 | (h1 << 16);
+          inf |= (hp[j] & 0x7fffu) == 0x7c00u || ((hp[j] >> 16) & 0x7fffu) == 0x7c00u;
+        *(uint32_t *)&vt_w[(4 * pd + j) * kVRow + 2 * pr] = hp[j];
       }
       if (HIST)
         v_range |= __any(inf); // wave-uniform
@@ -546,17 +588,17 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
 
 } // namespace gkv
 
-template <bool HIST>
+template <bool HIST, bool V8>
 static void launch_prefill(const gkv::PrefillArgs &a, int G, dim3 g, hipStream_t s) {
   using namespace gkv;
   if (G > 4)
-    hipLaunchKernelGGL((prefill_kernel<8, HIST>), g, dim3(512), 0, s, a);
+    hipLaunchKernelGGL((prefill_kernel<8, HIST, V8>), g, dim3(512), 0, s, a);
   else if (G > 2)
-    hipLaunchKernelGGL((prefill_kernel<4, HIST>), g, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((prefill_kernel<4, HIST, V8>), g, dim3(256), 0, s, a);
   else if (G > 1)
-    hipLaunchKernelGGL((prefill_kernel<2, HIST>), g, dim3(128), 0, s, a);
+    hipLaunchKernelGGL((prefill_kernel<2, HIST, V8>), g, dim3(128), 0, s, a);
   else
-    hipLaunchKernelGGL((prefill_kernel<1, HIST>), g, dim3(64), 0, s, a);
+    hipLaunchKernelGGL((prefill_kernel<1, HIST, V8>), g, dim3(64), 0, s, a);
 }
 
 // Query blocks per band of the grid order (2, or GKV_PREFILL_BAND, read
@@ -594,8 +636,11 @@ static int prefill_launch(void *stream, int32_t B, const int32_t *cu_seqlens,
     if (!cache->v || !cache->block_table || cache->table_stride <= 0 || cache->num_blocks <= 0 ||
         cache->n_kv_heads != n_kv_heads || cache->ring < 0)
       return GKV_ERR_ARG;
-    if (cache->v_format != GKV_V_BF16)
-      return GKV_ERR_UNSUPPORTED; // the prefill reads bf16 V
+    if (cache->v_format != GKV_V_BF16 && cache->v_format != GKV_V_INT8)
+      return GKV_ERR_UNSUPPORTED; // the prefill reads bf16 K
+    if ((cache->v_format == GKV_V_INT8) != (cache->v_scale != nullptr) ||
+        (uintptr_t)cache->v_scale % 16 != 0)
+      return GKV_ERR_ARG;
     if (cache->ring > 0 && (window != cache->ring || !k))
       return GKV_ERR_ARG; // a ring holds the history only: the chunk comes as packed rows
     if (((uintptr_t)cache->k | (uintptr_t)cache->v) % 16 != 0)
@@ -629,6 +674,7 @@ static int prefill_launch(void *stream, int32_t B, const int32_t *cu_seqlens,
   a.kv_stride = (int64_t)n_kv_heads * kHeadDim;
   a.kc = cached ? (const uint16_t *)cache->k : nullptr;
   a.vc = cached ? (const uint16_t *)cache->v : nullptr;
+  a.vs = cached ? (const float *)cache->v_scale : nullptr;
   a.table = cached ? cache->block_table : nullptr;
   a.table_stride = cached ? cache->table_stride : 0;
   a.num_blocks = cached ? cache->num_blocks : 0;
@@ -646,10 +692,12 @@ static int prefill_launch(void *stream, int32_t B, const int32_t *cu_seqlens,
   a.dev_err = dev_err;
   hipStream_t s = (hipStream_t)stream;
   const dim3 g((unsigned)grid);
-  if (cached)
-    launch_prefill<true>(a, G, g, s);
+  if (cached && cache->v_format == GKV_V_INT8)
+    launch_prefill<true, true>(a, G, g, s);
+  else if (cached)
+    launch_prefill<true, false>(a, G, g, s);
   else
-    launch_prefill<false>(a, G, g, s);
+    launch_prefill<false, false>(a, G, g, s);
   return launch_status("prefill_kernel");
 }
 

@@ -265,5 +265,10 @@ def test_prefill_paged_argument_checks(gkv):
     assert call(view=_view(gkv, k=None, v=None)) == gkv.GKV_ERR_ARG  # a history needs the cache
     assert call(view=_view(gkv, k=fake, v=fake, ring=128), window=0) == gkv.GKV_ERR_ARG
     assert call(view=_view(gkv, k=fake, v=fake, ring=128), window=64) == gkv.GKV_ERR_ARG
-    assert call(view=_view(gkv, k=fake, v=fake, v_format=1)) == gkv.GKV_ERR_UNSUPPORTED
+    # int8 V needs its scales (16-byte aligned); e4m3 K is not read by the prefill
+    assert call(view=_view(gkv, k=fake, v=fake, v_format=1)) == gkv.GKV_ERR_ARG
+    assert call(view=_view(gkv, k=fake, v=fake, v_format=1, v_scale=fake + 4)) == gkv.GKV_ERR_ARG
+    assert call(view=_view(gkv, k=fake, v=fake, v_format=0, v_scale=fake)) == gkv.GKV_ERR_ARG
+    assert call(view=_view(gkv, k=fake, v=fake, v_format=2, v_scale=fake)) == \
+        gkv.GKV_ERR_UNSUPPORTED
     assert call(B=0) == gkv.GKV_OK

@@ -12,6 +12,10 @@ every position, run.cpp:597-642) within max-abs 2e-3 + rel 1e-2.
   load slots past the block's last tile: they re-read cached blocks).
 - Ring layer (window 128): chunk 2 attended before it is appended (the ring
   still holds the last 128 positions of chunk 1), then appended.
+- The same three on the int8-V cache (the reference engine's format): the
+  keys read from the cache stand for code * scale (orc_quantize_v of the fp32
+  V, pinned to the reference's quantize_v), those from packed rows for their
+  bf16 values.
 - Error words: a start that is not a multiple of 16, and a V beyond the
   prefill's range.
 """
@@ -26,7 +30,8 @@ D = 64
 
 
 class Chunked:
-    def __init__(self, torch, gkv, oracle, L, C, Hq=64, Hkv=8, window=0, seed=0, scale=0.5):
+    def __init__(self, torch, gkv, oracle, L, C, Hq=64, Hkv=8, window=0, seed=0, scale=0.5,
+                 v_int8=False):
         rng = np.random.default_rng(seed)
         self.torch, self.gkv = torch, gkv
         self.L = np.asarray(L, np.int32)
@@ -40,14 +45,20 @@ class Chunked:
         pos = np.concatenate([np.arange(n) for n in self.L]).astype(np.int32)
         cos, sin = oracle.rope_table(int(self.L.max()))
         q_rot, _, kb, vb = oracle.kv_append(self.qkv, Hq, Hkv, cos, sin, pos)
-        self.ref = oracle.prefill_attention(cu, q_rot, oracle.from_bf16(kb), oracle.from_bf16(vb),
-                                            self.sinks, window=window)
+        self.oracle, self.q_rot, self.k_f = oracle, q_rot, oracle.from_bf16(kb)
+        self.v_bf = oracle.from_bf16(vb)
+        self.ref = oracle.prefill_attention(cu, q_rot, self.k_f, self.v_bf, self.sinks,
+                                            window=window)
+        self.v_int8 = v_int8
+        if v_int8:  # what the int8 cache stands for: the fp32 V quantized per token and head
+            v32 = self.qkv[:, (Hq + Hkv) * D:].reshape(T, Hkv, D)
+            self.v_q8 = oracle.dequantize_v(*oracle.quantize_v(v32))
         self.cu_all, self.pos = cu, pos
         # the pool: one layer (a ring layer when window > 0), NaN in every slot
         self.pool = gkv.Pool(n_layers=1, n_kv_heads=Hkv, max_seqs=self.B,
                              max_seq_len=int(self.L.max()), window=window,
                              num_blocks=int(((self.L + 15) // 16).sum()) + 8,
-                             shuffle_seed=seed + 3)
+                             shuffle_seed=seed + 3, v_format=gkv.V_INT8 if v_int8 else 0)
         for b in range(self.B):
             assert self.pool.seq_alloc() == b
             assert self.pool.reserve(b, int(self.L[b])) == 0
@@ -55,8 +66,10 @@ class Chunked:
         self.view = self.pool.view(0)
         n = self.view.num_blocks * Hkv * 16 * D
         nan = torch.full((n,), -1, dtype=torch.int16, device="cuda")  # bf16 0xffff: NaN
-        for base in (self.view.k, self.view.v):
-            gkv.hip_memcpy_d2d(base, nan.data_ptr(), n * 2)
+        gkv.hip_memcpy_d2d(self.view.k, nan.data_ptr(), n * 2)
+        gkv.hip_memcpy_d2d(self.view.v, nan.data_ptr(), n if v_int8 else n * 2)
+        if v_int8:  # int8 codes -1, scales NaN (fp32 0xffffffff)
+            gkv.hip_memcpy_d2d(self.view.v_scale, nan.data_ptr(), n // D * 4)
         torch.cuda.synchronize()
         t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to("cuda")  # noqa: E731
         self.t = t
@@ -108,8 +121,20 @@ class Chunked:
         torch.cuda.synchronize()
         return out.cpu().numpy()[:len(rows)].reshape(len(rows), self.Hq, D), rows
 
-    def check(self, got, rows, what):
-        bad, worst = allclose_report(got, self.ref[rows])
+    def ref_with_cache(self, rows, n_cached):
+        """The oracle's rows when the first n_cached[b] positions of prompt b
+        are read from an int8 cache (the rest from packed bf16 rows)."""
+        v = self.v_bf.copy()
+        for b in range(self.B):
+            lo = self.cu_all[b]
+            v[lo:lo + n_cached[b]] = self.v_q8[lo:lo + n_cached[b]]
+        return self.oracle.prefill_attention(self.cu_all, self.q_rot, self.k_f, v, self.sinks,
+                                             window=self.window)[rows]
+
+    def check(self, got, rows, what, n_cached=None):
+        want = self.ref[rows] if n_cached is None or not self.v_int8 else \
+            self.ref_with_cache(rows, n_cached)
+        bad, worst = allclose_report(got, want)
         assert bad == 0, f"{what}: {bad} outputs out of tolerance (max err {worst:.3e})"
         return worst
 
@@ -118,10 +143,11 @@ LENS = [300, 517, 64, 130, 1040, 33]
 CUTS = [128, 256, 48, 128, 512, 16]
 
 
+@pytest.mark.parametrize("v_int8", [False, True])
 @pytest.mark.parametrize("cache_only", [False, True])
-def test_two_chunks_full_layer(oracle, gkv, cuda, cache_only):
+def test_two_chunks_full_layer(oracle, gkv, cuda, cache_only, v_int8):
     import torch
-    c = Chunked(torch, gkv, oracle, LENS, CUTS, seed=11)
+    c = Chunked(torch, gkv, oracle, LENS, CUTS, seed=11, v_int8=v_int8)
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
     try:
         kp, vp = c.packed(1)
@@ -135,19 +161,21 @@ def test_two_chunks_full_layer(oracle, gkv, cuda, cache_only):
             kp, vp = c.packed(2)
             got, rows = c.prefill(2, err, k=kp, v=vp)  # history from the cache
             c.append(2, err)
-        w2 = c.check(got, rows, "chunk 2")
+        w2 = c.check(got, rows, "chunk 2", n_cached=c.L if cache_only else c.C)
         assert int(err.item()) == 0
-        print(f"full layer cache_only={cache_only}: max abs err {w1:.2e} / {w2:.2e}")
+        print(f"full layer cache_only={cache_only} v_int8={v_int8}: max abs err "
+              f"{w1:.2e} / {w2:.2e}")
     finally:
         c.pool.close()
 
 
-def test_two_chunks_ring_layer(oracle, gkv, cuda):
+@pytest.mark.parametrize("v_int8", [False, True])
+def test_two_chunks_ring_layer(oracle, gkv, cuda, v_int8):
     """Window 128 on a ring of 128 slots: chunk 2 attends to the ring's
     history before its own append overwrites it."""
     import torch
     c = Chunked(torch, gkv, oracle, [400, 700, 96, 260], [256, 512, 32, 128], window=128,
-                seed=12)
+                seed=12, v_int8=v_int8)
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
     try:
         kp, vp = c.packed(1)
@@ -157,7 +185,7 @@ def test_two_chunks_ring_layer(oracle, gkv, cuda):
         kp, vp = c.packed(2)
         got, rows = c.prefill(2, err, k=kp, v=vp)
         c.append(2, err)
-        c.check(got, rows, "chunk 2")
+        c.check(got, rows, "chunk 2", n_cached=c.C)
         assert int(err.item()) == 0
     finally:
         c.pool.close()
