@@ -314,7 +314,8 @@ def run_prefill(torch, gkv, args) -> int:
     need = int(((L + 15) // 16).sum())
     pool = gkv.Pool(n_layers=2, n_kv_heads=Hkv, max_seqs=B, max_seq_len=max_len,
                     window=cfg["window"], num_blocks=need + 64, shuffle_seed=args.seed,
-                    v_format=gkv.V_INT8 if args.v_int8 else gkv.V_BF16)
+                    v_format=gkv.KV_FP8 if args.kv_fp8 else
+                    gkv.V_INT8 if args.v_int8 else gkv.V_BF16)
     for b in range(B):
         assert pool.seq_alloc() == b
         if pool.reserve(b, int(L[b])) != 0:
@@ -404,7 +405,7 @@ def run_prefill(torch, gkv, args) -> int:
     alg_bytes = float(T * Hq * D * 4 + T * Hkv * D * 2 * 2 + T * Hq * D * 2)
     achieved = alg_bytes / (dom_ms * 1e-3) / 1e9
     traffic, traffic_note = load_traffic("prefill_config4_traffic")
-    if args.prefill_from_cache or args.v_int8:
+    if args.prefill_from_cache or args.v_int8 or args.kv_fp8:
         traffic, traffic_note = None, "the traffic profile covers packed rows and a bf16 cache"
     line = {
         "metric": "causal prefill attention throughput (TFLOP/s), config 4",
@@ -417,7 +418,8 @@ def run_prefill(torch, gkv, args) -> int:
         "config": {
             "workload": f"config 4: {cfg['name']}", "B": B, "H_q": Hq, "H_kv": Hkv,
             "head_dim": D, "prompt_tokens": T, "lengths": f"U[{cfg['lo']},{cfg['hi']}]",
-            "v_cache": "int8+scale" if args.v_int8 else "bf16",
+            "kv_cache": "e4m3 K and V + scales" if args.kv_fp8 else
+                        "bf16 K, int8+scale V" if args.v_int8 else "bf16",
             "full_layer_keys": "paged cache" if args.prefill_from_cache else "packed rows",
             "kernel_ms": {("window" if layers[i]["window"] else "full"): {
                 "append": round(float(np.mean([x[0] for x in kern[i]])), 4),

@@ -349,11 +349,10 @@ int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_seqlens, in
  * start_pos[b] + j and attends to positions max(0, p - W + 1) .. p, plus the
  * sink. start_pos: device int32 [B], multiples of 16 (else GKV_DEVERR_ALIGN
  * and the rows attend to themselves only), or NULL (all 0).
- *   keys before start_pos[b]  from the cache (gkv_cache_view with bf16 or int8
- *            V, GKV_V_BF16 / GKV_V_INT8: an int8 V stands for code * scale;
- *            GKV_KV_FP8 is GKV_ERR_UNSUPPORTED): the full layer's table, or a
- *            ring of W slots (cache.ring == window), which must still hold
- *            them -- append a ring layer's chunk after this call
+ *   keys before start_pos[b]  from the cache (gkv_cache_view in any format:
+ *            a quantized K or V stands for value(code) * scale): the full
+ *            layer's table, or a ring of W slots (cache.ring == window), which
+ *            must still hold them -- append a ring layer's chunk after this call
  *   keys from start_pos[b] on  from the packed rows k, v (bf16 [rows][Hkv][64],
  *            gkv_kv_append's k_pack/v_pack of this chunk); k = v = NULL: from
  *            the cache as well (a full layer whose chunk was appended first)

@@ -176,15 +176,6 @@ __device__ __forceinline__ u32x2 int8x4_to_bf16x4(uint32_t w) {
   return u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
 }
 
-// Four e4m3 codes (one per byte) -> four bf16 (exact: every e4m3 value is a
-// bf16 value), in order.
-__device__ __forceinline__ u32x2 fp8x4_to_bf16x4(uint32_t w) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
-  const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
-  return u32x2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
-}
-
 // ---- prep -----------------------------------------------------------------------
 
 // Query operands of sequence b, kv head g, for one wave. Lane (kg = lane/16,

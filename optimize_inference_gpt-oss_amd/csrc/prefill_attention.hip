@@ -74,7 +74,8 @@ struct PrefillArgs {
   const uint16_t *k, *v;          // packed rows (nullptr: every key from the cache)
   int64_t kv_stride; // elements per packed row: Hkv * 64
   const uint16_t *kc, *vc;        // the paged cache (K and V block layouts)
-  const float *vs;                // int8 V: the cache's V scales, [block][kv head][16]
+  const float *vs;                // the cache's scales: int8 V [block][kv head][16];
+                                  // e4m3 [block][kv head][32] (K scales, then V scales)
   const int32_t *table;
   int table_stride, num_blocks, ring;
   const float *sinks;
@@ -88,12 +89,14 @@ struct PrefillArgs {
 
 // HIST: prompts may continue a cached history (start positions, keys from
 // the cache); without it every key comes from the packed rows and the
-// history paths are compiled out. V8 (with HIST): the cache's V is int8
-// codes with a scale per token and head; a cached group's V stage then holds
-// the block's 1 KB of codes, then its 16 scales (64 bytes).
-template <int NW, bool HIST, bool V8 = false>
+// history paths are compiled out. VF (with HIST), the cache's storage: 0
+// bf16 K and V; 1 int8 V codes with a scale per token and head; 2 e4m3 K and
+// V codes, each with a scale per token and head. A cached group's stage of a
+// quantized K or V holds the block's 1 KB of codes, then its scales (int8 V:
+// 16 floats; e4m3: the block's 32, K scales then V scales).
+template <int NW, bool HIST, int VF = 0>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8 ? 4 : 1))) void prefill_kernel(PrefillArgs a) {
-  static_assert(HIST || !V8, "int8 V comes from the cache");
+  static_assert(HIST || VF == 0, "codes come from the cache");
   constexpr int D = kHeadDim;
   constexpr int NT = NW * 64;
   constexpr int kPieces = kKTile * D / 8 / NT; // V^T conversion: key pairs x 4 dims per thread
@@ -217,15 +220,16 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
         asm volatile("" : "+v"(lane_));
       const uint16_t *src;
       uint32_t off;
-      if (V8 && is_v && p < hist_end) {
-        // a cached int8 V block: half 0 its 1 KB of codes, half 1 its 16
-        // scales (lanes 0-3; the other lanes repeat them)
-        const int64_t blk = cached_block(ids, grp); // bf16 elements of a block = int8 bytes
+      if (VF != 0 && (is_v || VF == 2) && p < hist_end) {
+        // a cached block of codes: half 0 its 1 KB of codes, half 1 its
+        // scales (int8 V: 16 floats, lanes 0-3; e4m3: 32 floats, lanes 0-7;
+        // the other lanes repeat them)
+        const int64_t blk = cached_block(ids, grp); // bf16 elements of a block = code bytes
         if (half) {
-          src = (const uint16_t *)a.vs + blk / 32;
-          off = (lane_ & 3) * 8;
+          src = (const uint16_t *)a.vs + (VF == 2 ? blk / 16 : blk / 32);
+          off = (lane_ & (VF == 2 ? 7 : 3)) * 8;
         } else {
-          src = a.vc + blk / 2;
+          src = (is_v ? a.vc : a.kc) + blk / 2;
           off = lane_ * 8;
         }
       } else if (HIST && p < hist_end) {
@@ -279,13 +283,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
       const int r0 = 2 * pr, r1 = 2 * pr + 1;
       // dims 4pd + j of keys r0 (low half) and r1 (high half), as fp16 of v * 2^-10
       uint32_t hp[4];
-      if (V8 && kt0 + (r0 & ~(kBlockTokens - 1)) < hist_end) {
-        // int8 block: the codes of keys r0, r1 of dim d are adjacent bytes
-        // at ((d % 16) * 4 + t / 4) * 16 + (d / 16) * 4 + t % 4; the value is
-        // code * scale in fp32, as the cache stands for it. Slots past the
-        // block's last query position become 0.
+      if (VF != 0 && kt0 + (r0 & ~(kBlockTokens - 1)) < hist_end) {
+        // int8 or e4m3 block: the codes of keys r0, r1 of dim d are adjacent
+        // bytes at ((d % 16) * 4 + t / 4) * 16 + (d / 16) * 4 + t % 4; the
+        // value is value(code) * scale in fp32, as the cache stands for it.
+        // Slots past the block's last query position become 0.
         const uint16_t *blk = vs + (r0 >> 4) * 1024;
-        const float *scl = (const float *)(blk + 512);
+        const float *scl = (const float *)(blk + 512) + (VF == 2 ? kBlockTokens : 0);
         const int t0 = r0 & 15;
         const bool keep0 = kt0 + r0 <= p_last, keep1 = kt0 + r1 <= p_last;
         const float s0 = scl[t0], s1 = scl[t0 + 1];
@@ -295,8 +299,17 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
           const uint32_t c2 = *(const uint16_t *)((const char *)blk +
                                                   ((d & 15) * 4 + (t0 >> 2)) * 16 +
                                                   (d >> 4) * 4 + (t0 & 3));
-          const float x0 = keep0 ? (float)(int8_t)(c2 & 0xffu) * s0 : 0.0f;
-          const float x1 = keep1 ? (float)(int8_t)(c2 >> 8) * s1 : 0.0f;
+          float v0, v1;
+          if (VF == 2) {
+            const f32x2 f = __builtin_amdgcn_cvt_pk_f32_fp8((int)c2, false); // bytes 0, 1
+            v0 = f[0];
+            v1 = f[1];
+          } else {
+            v0 = (float)(int8_t)(c2 & 0xffu);
+            v1 = (float)(int8_t)(c2 >> 8);
+          }
+          const float x0 = keep0 ? v0 * s0 : 0.0f;
+          const float x1 = keep1 ? v1 * s1 : 0.0f;
           hp[j] = f32_half(x0) | (f32_half(x1) << 16);
         }
       } else {
@@ -421,16 +434,34 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
         // 32dh + 8kg .. +7: with a history (K staged in the block layout) 16
         // bytes at lane * 16 of half dh; else slot 4dh + kg of its swizzled row
         const int kr = 32 * s + 16 * kt + n;
+        // e4m3 codes of a cached group: lane (kg, n) holds key n's dims
+        // 8kg .. +7 (bytes 0-7) and 32 + 8kg .. +7 (bytes 8-15) at lane * 16;
+        // turned into bf16 exactly, the K scale applied to the scores
+        const bool f8 = VF == 2 && kb + 16 * kt < hist_end; // wave-uniform
 #pragma unroll
         for (int dh = 0; dh < 2; dh++) {
           const int ki = HIST ? (2 * s + kt) * 1024 + dh * 512 + lane * 8
                               : kr * D + 8 * ((4 * dh + kg) ^ (kr & 7));
-          const bf16x8 kop = *(const bf16x8 *)&ks[ki];
+          bf16x8 kop;
+          if (f8) {
+            const u32x2 w = *(const u32x2 *)((const char *)(ks + (2 * s + kt) * 1024) +
+                                             lane * 16 + dh * 8);
+            const u32x2 lo = fp8x4_to_bf16x4(w[0]), hi = fp8x4_to_bf16x4(w[1]);
+            kop = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+          } else {
+            kop = *(const bf16x8 *)&ks[ki];
+          }
 #pragma unroll
           for (int c = 0; c < 2; c++) {
             acc[kt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qhi[c][dh], acc[kt][c], 0, 0, 0);
             acc[kt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qlo[c][dh], acc[kt][c], 0, 0, 0);
           }
+        }
+        if (f8) { // keys 4kg .. 4kg+3 of the group: their K scales
+          const f32x4 ksc = *(const f32x4 *)((const float *)(ks + (2 * s + kt) * 1024 + 512) + 4 * kg);
+#pragma unroll
+          for (int c = 0; c < 2; c++)
+            acc[kt][c] *= ksc;
         }
       }
       f16x8 ph[2];
@@ -559,13 +590,17 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   if (!active)
     return;
 
-  // out = o * 2^(m - M) / (l * 2^(m - M) + 2^(sink - M)), M = max(m, sink)
+  // out = o * 2^(m - M) / (l * 2^(m - M) + 2^(sink - M)), M = max(m, sink).
+  // The query index is formed afresh here (kept from the query loads, it
+  // would hold a register through the tile loop).
+  int n_out = n;
+  asm volatile("" : "+v"(n_out));
 #pragma unroll
   for (int c = 0; c < 2; c++) {
     float ls = lsum[c];
     ls += __shfl_xor(ls, 16);
     ls += __shfl_xor(ls, 32);
-    const int qa = q0 + 16 * c + n;
+    const int qa = q0 + 16 * c + n_out;
     if (qa >= L)
       continue;
     const float M2 = fmaxf(m_run[c], sink2);
@@ -588,17 +623,17 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
 
 } // namespace gkv
 
-template <bool HIST, bool V8>
+template <bool HIST, int VF>
 static void launch_prefill(const gkv::PrefillArgs &a, int G, dim3 g, hipStream_t s) {
   using namespace gkv;
   if (G > 4)
-    hipLaunchKernelGGL((prefill_kernel<8, HIST, V8>), g, dim3(512), 0, s, a);
+    hipLaunchKernelGGL((prefill_kernel<8, HIST, VF>), g, dim3(512), 0, s, a);
   else if (G > 2)
-    hipLaunchKernelGGL((prefill_kernel<4, HIST, V8>), g, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((prefill_kernel<4, HIST, VF>), g, dim3(256), 0, s, a);
   else if (G > 1)
-    hipLaunchKernelGGL((prefill_kernel<2, HIST, V8>), g, dim3(128), 0, s, a);
+    hipLaunchKernelGGL((prefill_kernel<2, HIST, VF>), g, dim3(128), 0, s, a);
   else
-    hipLaunchKernelGGL((prefill_kernel<1, HIST, V8>), g, dim3(64), 0, s, a);
+    hipLaunchKernelGGL((prefill_kernel<1, HIST, VF>), g, dim3(64), 0, s, a);
 }
 
 // Query blocks per band of the grid order (2, or GKV_PREFILL_BAND, read
@@ -636,9 +671,10 @@ static int prefill_launch(void *stream, int32_t B, const int32_t *cu_seqlens,
     if (!cache->v || !cache->block_table || cache->table_stride <= 0 || cache->num_blocks <= 0 ||
         cache->n_kv_heads != n_kv_heads || cache->ring < 0)
       return GKV_ERR_ARG;
-    if (cache->v_format != GKV_V_BF16 && cache->v_format != GKV_V_INT8)
-      return GKV_ERR_UNSUPPORTED; // the prefill reads bf16 K
-    if ((cache->v_format == GKV_V_INT8) != (cache->v_scale != nullptr) ||
+    if (cache->v_format != GKV_V_BF16 && cache->v_format != GKV_V_INT8 &&
+        cache->v_format != GKV_KV_FP8)
+      return GKV_ERR_ARG;
+    if ((cache->v_format != GKV_V_BF16) != (cache->v_scale != nullptr) ||
         (uintptr_t)cache->v_scale % 16 != 0)
       return GKV_ERR_ARG;
     if (cache->ring > 0 && (window != cache->ring || !k))
@@ -692,12 +728,14 @@ static int prefill_launch(void *stream, int32_t B, const int32_t *cu_seqlens,
   a.dev_err = dev_err;
   hipStream_t s = (hipStream_t)stream;
   const dim3 g((unsigned)grid);
-  if (cached && cache->v_format == GKV_V_INT8)
-    launch_prefill<true, true>(a, G, g, s);
+  if (cached && cache->v_format == GKV_KV_FP8)
+    launch_prefill<true, 2>(a, G, g, s);
+  else if (cached && cache->v_format == GKV_V_INT8)
+    launch_prefill<true, 1>(a, G, g, s);
   else if (cached)
-    launch_prefill<true, false>(a, G, g, s);
+    launch_prefill<true, 0>(a, G, g, s);
   else
-    launch_prefill<false, false>(a, G, g, s);
+    launch_prefill<false, 0>(a, G, g, s);
   return launch_status("prefill_kernel");
 }
 

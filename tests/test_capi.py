@@ -164,16 +164,15 @@ def test_planned_layer_argument_checks(gkv):
         assert call(plan, B=0) == gkv.GKV_OK
 
 
-def test_fp8_cache_where_unsupported(gkv):
-    """The prefill over a history rejects the e4m3 cache; the appends need its
+def test_fp8_cache_needs_scales(gkv):
+    """The prefill over a history and the appends need the e4m3 cache's
     scales."""
     L = gkv.lib()
     fake = 0x1000
-    view = gkv.CacheView(fake, fake, fake, 8, 64, 8, 0, fake, gkv.KV_FP8)
-    st = L.gkv_prefill_paged(None, 1, fake, fake, 32, 64, fake, 5120, fake, fake, None, None,
-                             view, fake, 0, fake, 4096, 0, None)
-    assert st == gkv.GKV_ERR_UNSUPPORTED
     noscale = gkv.CacheView(fake, fake, fake, 8, 64, 8, 0, None, gkv.KV_FP8)
+    st = L.gkv_prefill_paged(None, 1, fake, fake, 32, 64, fake, 5120, fake, fake, None, None,
+                             noscale, fake, 0, fake, 4096, 0, None)
+    assert st == gkv.GKV_ERR_ARG
     st = L.gkv_qkv_append(None, 4, fake, 2880, 2880, fake, None, 64, fake, fake, None, None,
                           fake, noscale, fake, 5120, None)
     assert st == gkv.GKV_ERR_ARG  # the e4m3 cache needs its scales
@@ -265,10 +264,10 @@ def test_prefill_paged_argument_checks(gkv):
     assert call(view=_view(gkv, k=None, v=None)) == gkv.GKV_ERR_ARG  # a history needs the cache
     assert call(view=_view(gkv, k=fake, v=fake, ring=128), window=0) == gkv.GKV_ERR_ARG
     assert call(view=_view(gkv, k=fake, v=fake, ring=128), window=64) == gkv.GKV_ERR_ARG
-    # int8 V needs its scales (16-byte aligned); e4m3 K is not read by the prefill
+    # int8 V and e4m3 K/V need their scales (16-byte aligned), bf16 none; no other formats
     assert call(view=_view(gkv, k=fake, v=fake, v_format=1)) == gkv.GKV_ERR_ARG
+    assert call(view=_view(gkv, k=fake, v=fake, v_format=2)) == gkv.GKV_ERR_ARG
     assert call(view=_view(gkv, k=fake, v=fake, v_format=1, v_scale=fake + 4)) == gkv.GKV_ERR_ARG
     assert call(view=_view(gkv, k=fake, v=fake, v_format=0, v_scale=fake)) == gkv.GKV_ERR_ARG
-    assert call(view=_view(gkv, k=fake, v=fake, v_format=2, v_scale=fake)) == \
-        gkv.GKV_ERR_UNSUPPORTED
+    assert call(view=_view(gkv, k=fake, v=fake, v_format=3, v_scale=fake)) == gkv.GKV_ERR_ARG
     assert call(B=0) == gkv.GKV_OK

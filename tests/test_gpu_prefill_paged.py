@@ -12,10 +12,11 @@ every position, run.cpp:597-642) within max-abs 2e-3 + rel 1e-2.
   load slots past the block's last tile: they re-read cached blocks).
 - Ring layer (window 128): chunk 2 attended before it is appended (the ring
   still holds the last 128 positions of chunk 1), then appended.
-- The same three on the int8-V cache (the reference engine's format): the
-  keys read from the cache stand for code * scale (orc_quantize_v of the fp32
-  V, pinned to the reference's quantize_v), those from packed rows for their
-  bf16 values.
+- The same three on the int8-V cache (the reference engine's format) and on
+  the e4m3 K/V cache: the keys read from the cache stand for what the cache
+  holds (int8: code * scale, orc_quantize_v of the fp32 V, pinned to the
+  reference's quantize_v; e4m3: value(code) * scale of the rotated K and of
+  V, orc_quantize_fp8), those from packed rows for their bf16 values.
 - Error words: a start that is not a multiple of 16, and a V beyond the
   prefill's range.
 """
@@ -31,7 +32,7 @@ D = 64
 
 class Chunked:
     def __init__(self, torch, gkv, oracle, L, C, Hq=64, Hkv=8, window=0, seed=0, scale=0.5,
-                 v_int8=False):
+                 fmt="bf16"):
         rng = np.random.default_rng(seed)
         self.torch, self.gkv = torch, gkv
         self.L = np.asarray(L, np.int32)
@@ -44,21 +45,29 @@ class Chunked:
         self.sinks = rng.standard_normal(Hq).astype(np.float32)
         pos = np.concatenate([np.arange(n) for n in self.L]).astype(np.int32)
         cos, sin = oracle.rope_table(int(self.L.max()))
-        q_rot, _, kb, vb = oracle.kv_append(self.qkv, Hq, Hkv, cos, sin, pos)
+        q_rot, k_rot, kb, vb = oracle.kv_append(self.qkv, Hq, Hkv, cos, sin, pos)
         self.oracle, self.q_rot, self.k_f = oracle, q_rot, oracle.from_bf16(kb)
         self.v_bf = oracle.from_bf16(vb)
         self.ref = oracle.prefill_attention(cu, q_rot, self.k_f, self.v_bf, self.sinks,
                                             window=window)
-        self.v_int8 = v_int8
-        if v_int8:  # what the int8 cache stands for: the fp32 V quantized per token and head
-            v32 = self.qkv[:, (Hq + Hkv) * D:].reshape(T, Hkv, D)
-            self.v_q8 = oracle.dequantize_v(*oracle.quantize_v(v32))
+        # what a quantized cache stands for: the fp32 (rotated K and) V quantized per
+        # token and head
+        self.fmt = fmt
+        v32 = self.qkv[:, (Hq + Hkv) * D:].reshape(T, Hkv, D)
+        self.k_q, self.v_q = self.k_f, self.v_bf
+        if fmt == "int8":
+            self.v_q = oracle.dequantize_v(*oracle.quantize_v(v32))
+        elif fmt == "fp8":
+            self.k_q = oracle.dequantize_fp8(*oracle.quantize_fp8(k_rot.reshape(T, Hkv, D)))
+            self.v_q = oracle.dequantize_fp8(*oracle.quantize_fp8(v32))
         self.cu_all, self.pos = cu, pos
         # the pool: one layer (a ring layer when window > 0), NaN in every slot
         self.pool = gkv.Pool(n_layers=1, n_kv_heads=Hkv, max_seqs=self.B,
                              max_seq_len=int(self.L.max()), window=window,
                              num_blocks=int(((self.L + 15) // 16).sum()) + 8,
-                             shuffle_seed=seed + 3, v_format=gkv.V_INT8 if v_int8 else 0)
+                             shuffle_seed=seed + 3,
+                             v_format={"bf16": gkv.V_BF16, "int8": gkv.V_INT8,
+                                       "fp8": gkv.KV_FP8}[fmt])
         for b in range(self.B):
             assert self.pool.seq_alloc() == b
             assert self.pool.reserve(b, int(self.L[b])) == 0
@@ -66,10 +75,12 @@ class Chunked:
         self.view = self.pool.view(0)
         n = self.view.num_blocks * Hkv * 16 * D
         nan = torch.full((n,), -1, dtype=torch.int16, device="cuda")  # bf16 0xffff: NaN
-        gkv.hip_memcpy_d2d(self.view.k, nan.data_ptr(), n * 2)
-        gkv.hip_memcpy_d2d(self.view.v, nan.data_ptr(), n if v_int8 else n * 2)
-        if v_int8:  # int8 codes -1, scales NaN (fp32 0xffffffff)
-            gkv.hip_memcpy_d2d(self.view.v_scale, nan.data_ptr(), n // D * 4)
+        # codes 0xff (int8 -1, e4m3 NaN), scales NaN (fp32 0xffffffff)
+        gkv.hip_memcpy_d2d(self.view.k, nan.data_ptr(), n if fmt == "fp8" else n * 2)
+        gkv.hip_memcpy_d2d(self.view.v, nan.data_ptr(), n if fmt != "bf16" else n * 2)
+        if fmt != "bf16":
+            gkv.hip_memcpy_d2d(self.view.v_scale, nan.data_ptr(),
+                               n // D * (8 if fmt == "fp8" else 4))
         torch.cuda.synchronize()
         t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to("cuda")  # noqa: E731
         self.t = t
@@ -123,17 +134,22 @@ class Chunked:
 
     def ref_with_cache(self, rows, n_cached):
         """The oracle's rows when the first n_cached[b] positions of prompt b
-        are read from an int8 cache (the rest from packed bf16 rows)."""
-        v = self.v_bf.copy()
+        are read from a quantized cache (the rest from packed bf16 rows)."""
+        k, v = self.k_f.copy(), self.v_bf.copy()
         for b in range(self.B):
             lo = self.cu_all[b]
-            v[lo:lo + n_cached[b]] = self.v_q8[lo:lo + n_cached[b]]
-        return self.oracle.prefill_attention(self.cu_all, self.q_rot, self.k_f, v, self.sinks,
+            k[lo:lo + n_cached[b]] = self.k_q[lo:lo + n_cached[b]]
+            v[lo:lo + n_cached[b]] = self.v_q[lo:lo + n_cached[b]]
+        return self.oracle.prefill_attention(self.cu_all, self.q_rot, k, v, self.sinks,
                                              window=self.window)[rows]
 
     def check(self, got, rows, what, n_cached=None):
-        want = self.ref[rows] if n_cached is None or not self.v_int8 else \
+        want = self.ref[rows] if n_cached is None or self.fmt == "bf16" else \
             self.ref_with_cache(rows, n_cached)
+        if self.fmt == "fp8" and n_cached is not None:
+            # the e4m3 cache moves the output beyond the tolerance: the
+            # comparison tells the formats apart
+            assert allclose_report(want, self.ref[rows])[0] > 0
         bad, worst = allclose_report(got, want)
         assert bad == 0, f"{what}: {bad} outputs out of tolerance (max err {worst:.3e})"
         return worst
@@ -143,11 +159,11 @@ LENS = [300, 517, 64, 130, 1040, 33]
 CUTS = [128, 256, 48, 128, 512, 16]
 
 
-@pytest.mark.parametrize("v_int8", [False, True])
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "fp8"])
 @pytest.mark.parametrize("cache_only", [False, True])
-def test_two_chunks_full_layer(oracle, gkv, cuda, cache_only, v_int8):
+def test_two_chunks_full_layer(oracle, gkv, cuda, cache_only, fmt):
     import torch
-    c = Chunked(torch, gkv, oracle, LENS, CUTS, seed=11, v_int8=v_int8)
+    c = Chunked(torch, gkv, oracle, LENS, CUTS, seed=11, fmt=fmt)
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
     try:
         kp, vp = c.packed(1)
@@ -163,19 +179,19 @@ def test_two_chunks_full_layer(oracle, gkv, cuda, cache_only, v_int8):
             c.append(2, err)
         w2 = c.check(got, rows, "chunk 2", n_cached=c.L if cache_only else c.C)
         assert int(err.item()) == 0
-        print(f"full layer cache_only={cache_only} v_int8={v_int8}: max abs err "
+        print(f"full layer cache_only={cache_only} {fmt}: max abs err "
               f"{w1:.2e} / {w2:.2e}")
     finally:
         c.pool.close()
 
 
-@pytest.mark.parametrize("v_int8", [False, True])
-def test_two_chunks_ring_layer(oracle, gkv, cuda, v_int8):
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "fp8"])
+def test_two_chunks_ring_layer(oracle, gkv, cuda, fmt):
     """Window 128 on a ring of 128 slots: chunk 2 attends to the ring's
     history before its own append overwrites it."""
     import torch
     c = Chunked(torch, gkv, oracle, [400, 700, 96, 260], [256, 512, 32, 128], window=128,
-                seed=12, v_int8=v_int8)
+                seed=12, fmt=fmt)
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
     try:
         kp, vp = c.packed(1)
