@@ -148,6 +148,17 @@ def test_config4_shape(oracle, gkv, cuda, window):
     check(case, run_gpu(case, gkv, torch, cuda))
 
 
+@pytest.mark.parametrize("window", [0, 128])
+def test_config4_full_batch(oracle, gkv, cuda, window):
+    """Config 4 at its benchmark size: 64 prompts of U[64, 512] tokens (about
+    18k rows, 5,000+ workgroups), every output row against the oracle."""
+    import torch
+    rng = np.random.default_rng(400 + window)
+    lengths = rng.integers(64, 513, size=64)
+    case = PrefillCase(oracle, 401 + window, lengths, 64, 8, window=window)
+    check(case, run_gpu(case, gkv, torch, cuda))
+
+
 @pytest.mark.parametrize("window", [0, 16, 128])
 def test_edge_lengths(oracle, gkv, cuda, window):
     import torch
