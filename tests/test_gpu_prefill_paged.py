@@ -207,6 +207,30 @@ def test_two_chunks_ring_layer(oracle, gkv, cuda, fmt):
         c.pool.close()
 
 
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "fp8"])
+@pytest.mark.parametrize("Hq,Hkv", [(8, 2), (8, 4), (8, 8), (12, 2)])
+def test_group_sizes(oracle, gkv, cuda, Hq, Hkv, fmt):
+    """Groups of 4, 2, 1 and 6 query heads per kv head (the 4-, 2- and 1-wave
+    and a partly idle 8-wave workgroup of the history kernel), every cache
+    format: chunk 2 from packed rows over a cached history, then a full
+    re-read of both chunks from the cache."""
+    import torch
+    c = Chunked(torch, gkv, oracle, [150, 97, 33], [64, 80, 16], Hq=Hq, Hkv=Hkv,
+                seed=Hq * 10 + Hkv, fmt=fmt)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    try:
+        c.append(1, err)
+        kp, vp = c.packed(2)
+        got, rows = c.prefill(2, err, k=kp, v=vp)
+        c.check(got, rows, "chunk 2 over the cached history", n_cached=c.C)
+        c.append(2, err)
+        got, rows = c.prefill(2, err)
+        c.check(got, rows, "chunk 2 from the cache", n_cached=c.L)
+        assert int(err.item()) == 0
+    finally:
+        c.pool.close()
+
+
 def test_start_not_a_block_multiple_is_flagged(oracle, gkv, cuda):
     import torch
     c = Chunked(torch, gkv, oracle, [100, 80], [32, 48], seed=13)
