@@ -186,12 +186,13 @@ def test_two_chunks_full_layer(oracle, gkv, cuda, cache_only, fmt):
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "int8", "fp8"])
-def test_two_chunks_ring_layer(oracle, gkv, cuda, fmt):
-    """Window 128 on a ring of 128 slots: chunk 2 attends to the ring's
-    history before its own append overwrites it."""
+@pytest.mark.parametrize("window", [128, 32])
+def test_two_chunks_ring_layer(oracle, gkv, cuda, fmt, window):
+    """Window W on a ring of W slots: chunk 2 attends to the ring's history
+    before its own append overwrites it."""
     import torch
-    c = Chunked(torch, gkv, oracle, [400, 700, 96, 260], [256, 512, 32, 128], window=128,
-                seed=12, fmt=fmt)
+    c = Chunked(torch, gkv, oracle, [400, 700, 96, 260], [256, 512, 32, 128], window=window,
+                seed=12 + window, fmt=fmt)
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
     try:
         kp, vp = c.packed(1)
