@@ -536,6 +536,65 @@ def run_qkv(torch, gkv, args) -> int:
     return 0
 
 
+def run_yardsticks(torch, gkv, args, layer, lens_d, max_len, cos_d, sin_d, ws, layer_bytes,
+                   stream, step) -> int:
+    """Ceiling yardsticks next to the decode layer on the same box and run (the
+    reference quotes its decode kernel against its read_stream and loads-only
+    kernels, getp-csrc/bench/attn_bench.cpp:66-76,161-227):
+    - stream: a plain read of a buffer of the layer's K/V bytes;
+    - gather: the same buffer read as 2 KB blocks in a random order, one wave
+      per SIMD, 4 blocks per wave step (the decode kernel's unit and step);
+    - decode loads only: the layer's split launch with the attention math
+      replaced by an XOR (same plan, appends and loads; no combine);
+    - decode layer: the split launch as built (the attention), and the whole step.
+    Every figure is the mean of --steps launches, HIP events on the stream."""
+    dev = lens_d.device
+    n_bytes = int(layer_bytes) // 2048 * 2048
+    buf = torch.empty(n_bytes, dtype=torch.uint8, device=dev)
+    buf.view(torch.int32).random_()  # any data: only the reads are timed
+    sink = torch.zeros(256, dtype=torch.int32, device=dev)
+    g = torch.Generator().manual_seed(args.seed)
+    ids = torch.randperm(n_bytes // 2048, generator=g).to(torch.int32).to(dev)
+    n_cu = torch.cuda.get_device_properties(dev).multi_processor_count
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps * 1e3  # us
+
+    def decode(stage):
+        return lambda: gkv.decode_attention(layer.qkv, lens_d, max_len, layer.view, layer.sinks,
+                                            layer.out, window=layer.window, cos_tab=cos_d,
+                                            sin_tab=sin_d, workspace=ws, dev_err=err,
+                                            stream=stream, stage=stage)
+
+    res = {
+        "stream": (timed(lambda: gkv.yardstick_stream(buf, 4 * n_cu, sink, stream)), n_bytes),
+        "gather_2kb_random": (timed(lambda: gkv.yardstick_gather(buf, ids, n_cu, sink, stream)),
+                              n_bytes),
+        "decode_loads_only": (timed(decode("yardstick_loads")), layer_bytes),
+        "decode_split_launch": (timed(decode("layer_split")), layer_bytes),
+        "decode_step": (timed(lambda: step(False)), layer_bytes),
+    }
+    torch.cuda.synchronize()
+    line = {
+        "yardstick": f"config {args.config}, layer 0 (window {layer.window})",
+        "steps": args.steps, "warmup": args.warmup, "cus": n_cu,
+        "results": {k: {"us": round(us, 2), "bytes": b, "TB_s": round(b / (us * 1e-6) / 1e12, 3)}
+                    for k, (us, b) in res.items()},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -580,6 +639,10 @@ def main() -> int:
     ap.add_argument("--qkv-rows", type=int, default=0,
                     help="rows of the --qkv-projection run (default: config 2's 512 decode rows; "
                          "config 4's prompts hold 19024)")
+    ap.add_argument("--yardstick", action="store_true",
+                    help="ceiling yardsticks: a plain read and a random 2 KB-block gather of "
+                         "the layer's K/V bytes, and the decode launch with loads only, next "
+                         "to the decode launch and step as built")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="calibration mode: time a plain device copy of this many MiB "
                          "(the reference kernel for scaling rocprofv3 FETCH/WRITE_SIZE)")
@@ -716,6 +779,10 @@ def main() -> int:
     torch.cuda.synchronize()
     if int(err_d.item()) != 0:
         raise RuntimeError(f"device error word {int(err_d.item())}")
+
+    if args.yardstick:
+        return run_yardsticks(torch, gkv, args, layers[0], lens_d, max_len, cos_d, sin_d,
+                              ws_of[layers[0].window], bytes_of(layers[0]), stream, step)
 
     # Timed region: K steps, whole-step wall time (events only in a second pass,
     # so that the step time carries no event overhead).

@@ -281,11 +281,14 @@ int gkv_decode_layer_prepare(void *stream, int32_t B, int32_t n_q_heads, const f
  * prologue then only loads it and appends). GKV_PLAN_NONE is gkv_decode_layer.
  * Results are bit-identical to gkv_decode_layer's. Reuse needs the same
  * workspace, seq_lens and block_table pointers, B, window, split_tokens,
- * max_seq_len and pool shape as the keeping call, and unchanged lengths and
- * table contents; a launch that plans afresh on the workspace (any other
- * decode entry point) drops the kept plan. A key in the workspace checks the
- * shape and pointers: on a mismatch the call plans afresh and sets
- * GKV_DEVERR_PLAN; changed contents are not detected. Length errors
+ * max_seq_len and pool shape as the keeping call, and the same lengths; a
+ * launch that plans afresh on the workspace (any other decode entry point)
+ * drops the kept plan. A key in the workspace checks the shape, the pointers
+ * and a 64-bit hash of the lengths' contents: on a mismatch the call plans
+ * afresh (so its results are gkv_decode_layer's) and sets GKV_DEVERR_PLAN.
+ * The kept plan holds table positions, not block ids: a reusing call reads
+ * the ids from the table as it is at the call, so a changed table entry is
+ * used, not a stale one. Length errors
  * (GKV_DEVERR_LENGTH) are reported by the keeping call. Each kind needs a
  * workspace of its own (gkv_decode_workspace_bytes). */
 typedef enum { GKV_PLAN_NONE = 0, GKV_PLAN_KEEP = 1, GKV_PLAN_REUSE = 2 } gkv_plan_mode;
@@ -320,6 +323,36 @@ int gkv_decode_layer_noalloc(void *stream, int32_t B, int32_t n_q_heads, const f
                              const int32_t *seq_lens, int32_t max_seq_len, gkv_cache_view cache,
                              int32_t window, const float *sinks, void *out, int64_t out_stride,
                              int32_t out_dtype, uint32_t *dev_err);
+
+/* ---- Ceiling yardsticks ---------------------------------------------------- */
+
+/* Read-only kernels that measure what the memory system gives the decode
+ * kernel's access patterns, as the reference's attention bench does with its
+ * read_stream and loads-only kernels (getp-csrc/bench/attn_bench.cpp:66-76,
+ * 161-227). Each folds what it reads into an XOR and writes nothing
+ * meaningful to sink (device, >= 256 uint32). */
+/* Every byte of src (16-byte aligned, n_bytes a multiple of 16) once,
+ * nontemporal, 1 KB per wave instruction, over n_workgroups x 256 threads. */
+int gkv_yardstick_stream(void *stream, const void *src, int64_t n_bytes, int32_t n_workgroups,
+                         uint32_t *sink);
+/* The 2 KB blocks base + id * 2048 for the n_ids ids of block_ids (device;
+ * ids are clamped into the n_bytes of base), in steps of 4 blocks per wave,
+ * one wave per SIMD (n_workgroups x 4 waves), as the decode kernel reads one
+ * (block, kv head) of the paged cache. */
+int gkv_yardstick_gather(void *stream, const void *base, int64_t n_bytes,
+                         const int32_t *block_ids, int32_t n_ids, int32_t n_workgroups,
+                         uint32_t *sink);
+/* gkv_decode_layer's split launch (bf16 K/V only, else GKV_ERR_UNSUPPORTED)
+ * with the attention math replaced by an XOR of the loaded data: the same
+ * plan, appends and load stream (the appends are real; out is not written).
+ * No combine. */
+int gkv_yardstick_decode_loads(void *stream, int32_t B, int32_t n_q_heads, const float *qkv,
+                               int64_t row_stride, const float *cos_tab, const float *sin_tab,
+                               const int32_t *seq_lens, int32_t max_seq_len,
+                               gkv_cache_view cache, int32_t window, const float *sinks,
+                               int32_t split_tokens, void *workspace, size_t workspace_bytes,
+                               void *out, int64_t out_stride, int32_t out_dtype,
+                               uint32_t *dev_err);
 
 /* ---- Prefill (causal) attention ----------------------------------------- */
 

@@ -26,6 +26,7 @@ SOURCES = [
     "decode_attention.hip",
     "prefill_attention.hip",
     "qkv_append.hip",
+    "yardstick.hip",
     "rope_table.cpp",
     "kv_pool.cpp",
     "capi.cpp",
@@ -40,12 +41,11 @@ DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-p
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
     path = os.path.join(CSRC, src)
-    cmd = [HIPCC, *COMMON]
-    if src.endswith(".hip"):
-        cmd += ["-x", "hip", *DEVICE]
-    else:
-        cmd += ["-x", "hip", *DEVICE]  # host-only code; same driver keeps one toolchain
-    cmd += ["-c", path, "-o", obj]
+    # Every source, the host-only .cpp files included, compiles in HIP mode:
+    # rope_table.cpp must round like the reference's own hipcc build of
+    # run.cpp (HIP mode contracts a*b+c into FMAs, plain C++ mode does not),
+    # and the others use the HIP runtime headers either way.
+    cmd = [HIPCC, *COMMON, "-x", "hip", *DEVICE, "-c", path, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")

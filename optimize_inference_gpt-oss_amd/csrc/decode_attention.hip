@@ -71,7 +71,11 @@ namespace gkv {
 // step). Measured on the MI355X, a gather of random 2 KB blocks reads 6.9 TB/s
 // with it against 6.1 TB/s without, provided each load instruction covers
 // whole 128-byte lines (1 KB contiguous per wave).
+#ifndef GKV_KV_AUX
 constexpr int kKvAux = 2;
+#else
+constexpr int kKvAux = GKV_KV_AUX;
+#endif
 constexpr int kStep = 32;              // tokens per wave step
 constexpr int kCols = 8;               // query heads per kv head handled (G <= 8)
 constexpr int kMlStride = 16;          // floats of (m, l) per partial: 8 heads x 2
@@ -83,15 +87,19 @@ constexpr int kMaxRange = 16384;       // tokens per range (its ids and records 
 constexpr int kIdSlab = kMaxRange / kBlockTokens; // block ids per range (its slab in the workspace)
 constexpr int kInfoSlab = kMaxRange / kStep;      // step records per range
 constexpr int kSplitWaves = 4;         // split kernel: one wave per SIMD
+constexpr int kStageRecs = 8;          // finished segments a stream wave holds in LDS
 constexpr int kSplitThreads = 64 * kSplitWaves;
 constexpr int kPrepThreads = 1024;
 constexpr int kMaxBatch = 8192;        // sequences per call (prefix sums kept in LDS)
 constexpr int kBadBlock = -1;          // F entry: id outside the pool
 constexpr int kPadBlock = -2;          // F entry: no tokens (padding)
 // A decode layer's plan kept for the following layers of its kind (the same
-// lengths and table): a key naming what it was built for, then each range's
-// bounds, first sequence and count of sequences; the block ids and step
-// records stay in the range slabs (flat, steps).
+// lengths): a key naming what it was built for (the shape, the pointers and a
+// hash of the lengths' contents), then each range's bounds, first sequence and
+// count of sequences; the step records and the table position of every block
+// (row * table_stride + column, not the id it held: a reusing launch reads the
+// ids from the table afresh, so a changed table entry is never stale) stay in
+// the range slabs (flat, steps).
 constexpr int kKeyInts = 16;
 constexpr int kPlanMagic = 0x504c4e31;
 constexpr int kKeepPlan = 2;           // fused launch mode bits (bit 0: append)
@@ -415,7 +423,10 @@ __global__ __launch_bounds__(kPrepThreads) void decode_layer_prep_kernel(DecodeA
 // pieces prepared by the prepare launch (a.qops).
 // VF: the cache's value format, 0 bf16 K/V, 1 int8 V (+ scales), 2 e4m3 K and
 // V (+ scales).
-template <int R, int VF, bool RAWQ>
+// LO: loads only (the ceiling yardstick): every load of the stream is issued
+// and waited for exactly as in the attention, and its data is folded into an
+// XOR instead of the softmax and the matrix ops; nothing useful is written.
+template <int R, int VF, bool RAWQ, bool LO = false>
 __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, const int2 *s_ids,
                                              const int *s_rec, const int *s_len, int n_steps) {
   constexpr int D = kHeadDim;
@@ -572,8 +583,61 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
   for (int nn = 0; nn < 4; nn++)
     o[nn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // Finished segments wait in LDS and go to memory after the stream: a
+  // global store among the stream's loads delays the loads behind it (about
+  // 2.5 us per segment measured on config 2, 15 us per launch), an LDS write
+  // does not. Record r of this wave: the 16 values of each of the 32 lanes
+  // that hold outputs (lane (kg, col < 8): query head col, dims 4 kg + 16 nn
+  // + 0..3), the (m, l) of each query head for a partial, and what the record
+  // is (a whole sequence's output, scaled, or a partial for the combine).
+  __shared__ f32x4 s_st_o[kSplitWaves][kStageRecs][32][4];
+  __shared__ float2 s_st_ml[kSplitWaves][kStageRecs][kCols];
+  __shared__ int4 s_st_meta[kSplitWaves][kStageRecs];
+  int n_staged = 0; // wave-uniform
+  const bool out_lane = !lo && head_ok;
+  const int st_lane = kg * 8 + head;
+
+  // Writes the staged records to memory: outputs (bf16 or fp32) and partials.
+  auto write_out = [&]() {
+    for (int r = 0; r < n_staged; r++) {
+      const int4 m = s_st_meta[wv][r]; // {whole, sequence, kv head, partial index}
+      if (!out_lane)
+        continue;
+      f32x4 oo[4];
+#pragma unroll
+      for (int nn = 0; nn < 4; nn++)
+        oo[nn] = s_st_o[wv][r][st_lane][nn];
+      if (m.x) {
+        const int64_t ob = (int64_t)m.y * a.out_stride + (int64_t)(m.z * a.G + head) * D + 4 * kg;
+#pragma unroll
+        for (int nn = 0; nn < 4; nn++) {
+          if (a.out_bf16) {
+            typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+            *(bf16x4 *)((__bf16 *)a.out + ob + 16 * nn) =
+                bf16x4{(__bf16)oo[nn][0], (__bf16)oo[nn][1], (__bf16)oo[nn][2],
+                       (__bf16)oo[nn][3]};
+          } else {
+            *(f32x4 *)((float *)a.out + ob + 16 * nn) = oo[nn];
+          }
+        }
+      } else {
+        const int64_t part = m.w;
+        float *wo = a.ws_o + part * kPartFloats + head * D + 4 * kg;
+#pragma unroll
+        for (int nn = 0; nn < 4; nn++)
+          *(f32x4 *)(wo + 16 * nn) = oo[nn];
+        if (kg == 0) {
+          const float2 ml = s_st_ml[wv][r][head];
+          a.ws_ml[part * kMlStride + 2 * head] = ml.x;
+          a.ws_ml[part * kMlStride + 2 * head + 1] = ml.y;
+        }
+      }
+    }
+    n_staged = 0;
+  };
+
   // Finishes the open segment: the output (sink added) if it is the whole
-  // sequence, else the partial for the combine.
+  // sequence, else the partial for the combine; staged in LDS.
   auto flush = [&]() {
     float ls = lsum;
     ls += __shfl_xor(ls, 16);
@@ -584,44 +648,51 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
 #pragma unroll
       for (int r = 0; r < 4; r++)
         oo[nn][r] = o[nn][r] + swap8(o[nn][r]);
-    if (lo || !head_ok || cur_key < 0)
+    if (cur_key < 0)
       return;
-    const int hq = cur_g * a.G + head;
-    if (cur_whole && cur_ends) {
-      // out = o * 2^(m - M) / (l * 2^(m - M) + 2^(sink - M)), M = max(m, sink)
-      const float M2 = fmaxf(m_run, cur_sink);
-      const float f = __builtin_amdgcn_exp2f(m_run - M2);
-      const float scale = f / fmaf(ls, f, __builtin_amdgcn_exp2f(cur_sink - M2));
-      const int64_t ob = (int64_t)cur_b * a.out_stride + (int64_t)hq * D + 4 * kg;
-#pragma unroll
-      for (int nn = 0; nn < 4; nn++) {
-        if (a.out_bf16) {
-          typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-          *(bf16x4 *)((__bf16 *)a.out + ob + 16 * nn) =
-              bf16x4{(__bf16)(oo[nn][0] * scale), (__bf16)(oo[nn][1] * scale),
-                     (__bf16)(oo[nn][2] * scale), (__bf16)(oo[nn][3] * scale)};
-        } else {
-          *(f32x4 *)((float *)a.out + ob + 16 * nn) = oo[nn] * scale;
-        }
+    if (n_staged == kStageRecs) // full (many short sequences): to memory now
+      write_out();
+    const bool whole = cur_whole && cur_ends;
+    if (out_lane) {
+      float scale = 1.0f;
+      if (whole) {
+        // out = o * 2^(m - M) / (l * 2^(m - M) + 2^(sink - M)), M = max(m, sink)
+        const float M2 = fmaxf(m_run, cur_sink);
+        const float f = __builtin_amdgcn_exp2f(m_run - M2);
+        scale = f / fmaf(ls, f, __builtin_amdgcn_exp2f(cur_sink - M2));
+      } else if (kg == 0) {
+        s_st_ml[wv][n_staged][head] = float2{m_run, ls};
       }
-    } else {
-      // only a range's first and last segments can be pieces of a longer
-      // sequence: partial slot 0 for the first, 1 for the last
-      const int64_t part =
-          ((int64_t)w_id * kPartsPerRange + (cur_first ? 0 : 1)) * a.n_kv_heads + cur_g;
-      float *wo = a.ws_o + part * kPartFloats + head * D + 4 * kg;
 #pragma unroll
       for (int nn = 0; nn < 4; nn++)
-        *(f32x4 *)(wo + 16 * nn) = oo[nn];
-      if (kg == 0) {
-        a.ws_ml[part * kMlStride + 2 * head] = m_run;
-        a.ws_ml[part * kMlStride + 2 * head + 1] = ls;
-      }
+        s_st_o[wv][n_staged][st_lane][nn] = whole ? oo[nn] * scale : oo[nn];
     }
+    if (lane == 0) {
+      // only a range's first and last segments can be pieces of a longer
+      // sequence: partial slot 0 for the first, 1 for the last
+      const int part = (w_id * kPartsPerRange + (cur_first ? 0 : 1)) * a.n_kv_heads + cur_g;
+      s_st_meta[wv][n_staged] = int4{whole ? 1 : 0, cur_b, cur_g, part};
+    }
+    n_staged++;
   };
 
+  uint32_t lo_acc = 0; // LO: the XOR of everything loaded
   auto compute_step = [&](u32x4 (&kr)[4], u32x4 (&vr)[4], u32x4 (&qr)[QN], int rc, int bb,
                           int v) {
+    if constexpr (LO) {
+      // a multiply per step keeps the steps in order (an XOR chain alone
+      // would let the compiler regroup it and wait for later steps' loads)
+      uint32_t x = (uint32_t)(rc ^ bb);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          x ^= kr[i][j] ^ vr[i][j];
+      lo_acc = (lo_acc ^ x) * 0x01000193u;
+      // and no instruction moves across the step: the ring stays a ring
+      __builtin_amdgcn_sched_barrier(0);
+      return;
+    }
     const bool in_range = v <= last_v;
     const int pass = bb >> 2;
     const int key = (rc >> 8) | (pass << 16);
@@ -801,7 +872,14 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
       compute_step(kbuf[r], vbuf[r], qbuf[r], rec[r], badb[r], v);
     }
   }
+  if constexpr (LO) {
+    // a store the compiler cannot drop, which (practically) never happens
+    if (lo_acc == 0x9e3779b9u)
+      ((uint32_t *)a.out)[lane] = lo_acc;
+    return;
+  }
   flush();
+  write_out();
 }
 
 // The split launch of the staged path: the plan, block ids and step records
@@ -845,9 +923,49 @@ __device__ __forceinline__ int stream_tokens(const DecodeArgs &a, int L) {
   return max(min(n, min(a.table_stride * kBlockTokens, a.max_len)), 0);
 }
 
-// Word i of a kept plan's key: what the plan depends on besides the contents
-// of the lengths and of the table.
-__device__ __forceinline__ int plan_key(const DecodeArgs &a, int i) {
+// Murmur3's 32-bit finaliser: a bijection of the 32-bit words.
+__device__ __forceinline__ uint32_t fmix32(uint32_t h) {
+  h ^= h >> 16;
+  h *= 0x85ebca6bu;
+  h ^= h >> 13;
+  h *= 0xc2b2ae35u;
+  h ^= h >> 16;
+  return h;
+}
+
+// Hash of the B lengths, the same in every workgroup: two sums over b of a
+// bijective mix of (b, L_b), so that one changed length always changes both
+// and several collide with probability ~2^-64. Called by the whole workgroup
+// (it holds two barriers); s_red holds 2 ints per wave.
+__device__ uint2 lengths_hash(const DecodeArgs &a, int *s_red) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, n_waves = blockDim.x >> 6;
+  uint32_t h0 = 0, h1 = 0;
+  for (int b = t; b < a.B; b += blockDim.x) {
+    const uint32_t L = (uint32_t)a.seq_lens[b];
+    h0 += fmix32(L ^ ((uint32_t)b * 0x9e3779b9u));
+    h1 += fmix32((L + 0x7f4a7c15u) ^ ((uint32_t)b * 0x632be5abu) ^ 0x5bd1e995u);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    h0 += (uint32_t)__shfl_xor((int)h0, off);
+    h1 += (uint32_t)__shfl_xor((int)h1, off);
+  }
+  __syncthreads(); // s_red may hold an earlier call's sums
+  if (lane == 0) {
+    s_red[2 * wave] = (int)h0;
+    s_red[2 * wave + 1] = (int)h1;
+  }
+  __syncthreads();
+  h0 = h1 = 0;
+  for (int w = 0; w < n_waves; w++) {
+    h0 += (uint32_t)s_red[2 * w];
+    h1 += (uint32_t)s_red[2 * w + 1];
+  }
+  return uint2{h0, h1};
+}
+
+// Word i of a kept plan's key: the shape, the pointers and the lengths' hash.
+__device__ __forceinline__ int plan_key(const DecodeArgs &a, int i, uint2 lh) {
   const uint64_t lens = (uint64_t)(uintptr_t)a.seq_lens, tab = (uint64_t)(uintptr_t)a.table;
   switch (i) {
   case 0: return kPlanMagic;
@@ -864,6 +982,8 @@ __device__ __forceinline__ int plan_key(const DecodeArgs &a, int i) {
   case 11: return (int)(uint32_t)(lens >> 32);
   case 12: return (int)(uint32_t)tab;
   case 13: return (int)(uint32_t)(tab >> 32);
+  case 14: return (int)lh.x;
+  case 15: return (int)lh.y;
   default: return 0;
   }
 }
@@ -879,12 +999,15 @@ __device__ __forceinline__ int plan_key(const DecodeArgs &a, int i) {
 // stream belongs to one range). Workgroup 0 publishes the plan for the
 // combine.
 // mode: bit 0 append; kKeepPlan: also keep the plan in the workspace (each
-// range's bounds, block ids and step records, under a key); kReusePlan: take
-// the kept plan instead of planning, when its key matches this launch (else
-// plan afresh and report GKV_DEVERR_PLAN). Layers of one kind in one decode
-// step share the lengths and the table, so one keeps and the others reuse;
-// the ranges, and so every output bit, are the same either way.
-template <int R, int VF>
+// range's bounds, table positions and step records, under a key); kReusePlan:
+// take the kept plan instead of planning, when its key (the lengths' hash
+// included) matches this launch, else plan afresh and report GKV_DEVERR_PLAN.
+// A reusing launch reads the block ids from the table at the kept positions,
+// so a table changed since the plan was kept is read as it is now. Layers of
+// one kind in one decode step share the lengths and the table, so one keeps
+// and the others reuse; the ranges, and so every output bit, are the same
+// either way.
+template <int R, int VF, bool LO = false>
 __global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(1)))
 void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
   __shared__ int s_cu[kMaxBatch + 1];
@@ -893,6 +1016,7 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
   __shared__ int s_rec[kInfoSlab];
   __shared__ int s_wave[kSplitWaves];
   __shared__ int s_max[kSplitWaves];
+  __shared__ int s_hash[2 * kSplitWaves];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nt = blockDim.x, B = a.B;
   const int n_waves = nt >> 6;
   const int w_id = blockIdx.x;
@@ -901,10 +1025,11 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
 
   bool reuse = false;
   if (mode & kReusePlan) {
+    const uint2 lh = lengths_hash(a, s_hash);
     bool same = true;
 #pragma unroll
     for (int i = 0; i < kKeyInts; i++)
-      same &= a.kept[i] == plan_key(a, i);
+      same &= a.kept[i] == plan_key(a, i, lh);
     reuse = uniform(same);
     if (!reuse && w_id == 0 && t == 0 && a.dev_err)
       atomicOr(a.dev_err, GKV_DEVERR_PLAN);
@@ -992,10 +1117,13 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
       }
       // a kept plan is valid until a launch plans afresh on this workspace
       if (a.kept) {
-        if (keep && t < kKeyInts)
-          a.kept[t] = plan_key(a, t);
-        else if (!keep && t == 0)
+        if (keep) {
+          const uint2 lh = lengths_hash(a, s_hash);
+          if (t < kKeyInts)
+            a.kept[t] = plan_key(a, t, lh);
+        } else if (t == 0) {
           a.kept[0] = 0;
+        }
       }
       if (any_over && a.dev_err)
         atomicOr(a.dev_err, GKV_DEVERR_LENGTH);
@@ -1128,20 +1256,26 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
   // Step records and block ids of the range (the table loads, or the kept
   // slabs' loads, go out here).
   int id0[kStepsPerThread], id1[kStepsPerThread], rcd[kStepsPerThread];
+  int pos0[kStepsPerThread], pos1[kStepsPerThread]; // table positions (kept plans)
   if (reuse) {
+    // the kept table positions, then the ids they hold now
     const int2 *src = (const int2 *)(a.flat + (int64_t)w_id * kIdSlab);
     const int *srec = a.steps + (int64_t)w_id * kInfoSlab;
+    int2 pos[kStepsPerThread];
 #pragma unroll
     for (int k = 0; k < kStepsPerThread; k++) {
       const int i = t + k * nt;
-      id0[k] = id1[k] = kPadBlock;
+      pos[k] = int2{kPadBlock, kPadBlock};
       rcd[k] = 0;
       if (i < n_steps) {
-        const int2 p = src[i];
-        id0[k] = p.x;
-        id1[k] = p.y;
+        pos[k] = src[i];
         rcd[k] = srec[i];
       }
+    }
+#pragma unroll
+    for (int k = 0; k < kStepsPerThread; k++) {
+      id0[k] = pos[k].x >= 0 ? a.table[pos[k].x] : kPadBlock;
+      id1[k] = pos[k].y >= 0 ? a.table[pos[k].y] : kPadBlock;
     }
     for (int j = t; j < n_seq; j += nt)
       s_len[b_first + j] = a.seq_lens[b_first + j];
@@ -1150,6 +1284,7 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
     for (int k = 0; k < kStepsPerThread; k++) {
       const int i = t + k * nt;
       id0[k] = id1[k] = kPadBlock;
+      pos0[k] = pos1[k] = kPadBlock;
       rcd[k] = 0;
       if (i < n_steps) {
         const int tok = rs + i * kStep;
@@ -1164,11 +1299,15 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
         const int b = lo;
         const int off = tok - s_cu[b];
         const int n = stream_tokens(a, s_len[b]);
-        const int32_t *row = a.table + (int64_t)b * a.table_stride + off / kBlockTokens;
-        if (off < n)
-          id0[k] = row[0];
-        if (off + kBlockTokens < n)
-          id1[k] = row[1];
+        const int p0 = b * a.table_stride + off / kBlockTokens;
+        if (off < n) {
+          id0[k] = a.table[p0];
+          pos0[k] = p0;
+        }
+        if (off + kBlockTokens < n) {
+          id1[k] = a.table[p0 + 1];
+          pos1[k] = p0 + 1;
+        }
         rcd[k] = step_record(b, off == 0, tok + kStep == s_cu[b + 1], min(max(n - off, 0), kStep));
       }
     }
@@ -1201,8 +1340,8 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
       }
       s_ids[i] = int2{x, y};
       s_rec[i] = rcd[k];
-      if (keep) {
-        ((int2 *)(a.flat + (int64_t)w_id * kIdSlab))[i] = int2{x, y};
+      if (keep && !reuse) {
+        ((int2 *)(a.flat + (int64_t)w_id * kIdSlab))[i] = int2{pos0[k], pos1[k]};
         a.steps[(int64_t)w_id * kInfoSlab + i] = rcd[k];
       }
     }
@@ -1223,7 +1362,7 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
   KernargPtr pa = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
   asm volatile("" : "+s"(pa));
   const DecodeArgs a2 = *pa;
-  stream_range<R, VF, true>(a2, w_id, s_ids, s_rec, s_len, n_steps);
+  stream_range<R, VF, true, LO>(a2, w_id, s_ids, s_rec, s_len, n_steps);
 #endif
 }
 
@@ -1742,6 +1881,21 @@ extern "C" int gkv_decode_layer(GKV_LAYER_PARAMS) {
 
 static int plan_bits(int32_t plan) {
   return plan == GKV_PLAN_KEEP ? kKeepPlan : plan == GKV_PLAN_REUSE ? kReusePlan : 0;
+}
+
+// The loads-only form of gkv_decode_layer's split launch (bf16 K/V): the same
+// plan, appends and load stream, the attention math replaced by an XOR of the
+// loaded data. A ceiling yardstick, as the reference's loads-only kernels
+// (getp-csrc/bench/attn_bench.cpp:161-227); the outputs are not written.
+extern "C" int gkv_yardstick_decode_loads(GKV_LAYER_PARAMS) {
+  if (cache.v_format != GKV_V_BF16)
+    return GKV_ERR_UNSUPPORTED;
+  GKV_LAYER_SETUP
+  AppendArgs aa = ap;
+  aa.seq_lens = nullptr;
+  hipLaunchKernelGGL((decode_fused_kernel<4, 0, true>), dim3(a.n_wg),
+                     dim3(split_block(a.n_kv_heads)), 0, (hipStream_t)stream, a, aa, 1);
+  return launch_status("decode_fused_kernel (loads only)");
 }
 
 extern "C" int gkv_decode_layer_planned(GKV_LAYER_PARAMS, int32_t plan) {

@@ -118,6 +118,11 @@ SIGNATURES = {
     "gkv_decode_split": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp, _i32,
                                         CacheView, _i32, _vp, _i32, _vp, _sz, _vp, _i64, _i32,
                                         _vp]),
+    "gkv_yardstick_decode_loads": (ctypes.c_int, [_vp, _i32, _i32, _vp, _i64, _vp, _vp, _vp,
+                                                  _i32, CacheView, _i32, _vp, _i32, _vp, _sz,
+                                                  _vp, _i64, _i32, _vp]),
+    "gkv_yardstick_stream": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp]),
+    "gkv_yardstick_gather": (ctypes.c_int, [_vp, _vp, _i64, _vp, _i32, _i32, _vp]),
     "gkv_decode_combine": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _i32, _i32, _vp, _i32,
                                           _vp, _sz, _vp, _i64, _i32]),
     "gkv_prefill_attention": (ctypes.c_int, [_vp, _i32, _vp, _i32, _i32, _i32, _vp, _i64, _vp,
@@ -265,6 +270,21 @@ def qkv_append(x, w_qkv, b_qkv, n_q_heads, cos_tab, sin_tab, view: CacheView | N
     check("gkv_qkv_append", st)
 
 
+def yardstick_stream(buf, n_workgroups, sink, stream=None):
+    """gkv_yardstick_stream: read every byte of buf (a device tensor) once."""
+    st = lib().gkv_yardstick_stream(stream_handle(stream), ptr(buf),
+                                    buf.numel() * buf.element_size(), n_workgroups, ptr(sink))
+    check("gkv_yardstick_stream", st)
+
+
+def yardstick_gather(buf, block_ids, n_workgroups, sink, stream=None):
+    """gkv_yardstick_gather: read the 2 KB blocks of buf listed in block_ids."""
+    st = lib().gkv_yardstick_gather(stream_handle(stream), ptr(buf),
+                                    buf.numel() * buf.element_size(), ptr(block_ids),
+                                    block_ids.numel(), n_workgroups, ptr(sink))
+    check("gkv_yardstick_gather", st)
+
+
 def workspace_bytes(B, n_kv_heads, max_seq_len, window=0, split_tokens=0) -> int:
     return lib().gkv_decode_workspace_bytes(B, n_kv_heads, max_seq_len, window, split_tokens)
 
@@ -284,11 +304,13 @@ def decode_attention(q, seq_lens, max_seq_len, view: CacheView, sinks, out, wind
     out_dtype = BF16 if out.dtype == torch.bfloat16 else F32
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     args_common = (stream_handle(stream), q.shape[0])
-    if stage in ("both", "prepare", "split", "layer", "layer_prepare", "layer_split"):
+    if stage in ("both", "prepare", "split", "layer", "layer_prepare", "layer_split",
+                 "yardstick_loads"):
         name = {"both": "gkv_decode_attention", "prepare": "gkv_decode_prepare",
                 "split": "gkv_decode_split", "layer": "gkv_decode_layer",
                 "layer_prepare": "gkv_decode_layer_prepare",
-                "layer_split": "gkv_decode_layer_split"}[stage]
+                "layer_split": "gkv_decode_layer_split",
+                "yardstick_loads": "gkv_yardstick_decode_loads"}[stage]
         st = getattr(lib(), name)(*args_common, sinks.shape[0], ptr(q), q.stride(0),
                                   ptr(cos_tab), ptr(sin_tab), ptr(seq_lens), max_seq_len, view,
                                   window, ptr(sinks), split_tokens, ptr(workspace), ws_bytes,

@@ -8,6 +8,10 @@ split launch's plan once (GKV_PLAN_KEEP) and reuse it (GKV_PLAN_REUSE).
 - A reuse the workspace does not hold a plan for (a plain call planned on it
   since, or another batch size) plans afresh, gives the same bits and sets
   GKV_DEVERR_PLAN.
+- A plan reused after the table changed behind the same pointer reads the
+  moved block where the table now points (oracle parity, no error); after a
+  length changed, the reuse plans afresh (the plain call's bits, the error
+  bit set): the key holds a hash of the lengths.
 - Config 5's shape (B=1024, contexts U[1024, 3072], window and full layers
   alternating, one workspace per kind): four layers kept/reused against four
   plain calls, outputs and both pool arrays bit for bit.
@@ -156,3 +160,83 @@ def test_config5_layers_keep_and_reuse(gkv, cuda, torch_mod):
             del k1, v1
     finally:
         P.close()
+
+
+@pytest.mark.parametrize("window", [0, 128])
+def test_reuse_sees_changed_table_and_lengths(gkv, cuda, torch_mod, window):
+    """A plan kept at one call and reused after the table or the lengths
+    changed behind the same pointers: a moved block is read where the table
+    now points (oracle parity, no error), a changed length makes the reuse
+    plan afresh (the plain call's bits, GKV_DEVERR_PLAN set)."""
+    from kvcase import allclose_report
+    torch = torch_mod
+    rng = np.random.default_rng(310 + window)
+    B = 300
+    L = rng.integers(1, 1500 if window == 0 else 400, size=B).astype(np.int32)
+    print(f"stale reuse window={window} B={B}", flush=True)
+    case = DecodeCase(B, 64, 8, L, window=window, scale=0.5, seed=311)
+    max_len = int(case.seq_lens.max())
+    cos, sin = gkv.rope_table(case.cos.shape[0])
+    dev = case.to_device(torch, cuda, cos, sin)
+    view = gkv.cache_view(dev["k"], dev["v"], dev["table"], case.Hkv, ring=case.ring)
+    nbytes = gkv.workspace_bytes(B, 8, max_len, window, 0)
+    ws_plain = torch.empty(nbytes, dtype=torch.uint8, device=cuda)
+    ws_plan = torch.empty(nbytes, dtype=torch.uint8, device=cuda)
+    snap = [dev["k"].clone(), dev["v"].clone()]
+
+    def restore():
+        dev["k"].copy_(snap[0])
+        dev["v"].copy_(snap[1])
+
+    def run(lens, plan=None):
+        out = torch.full((B, case.Hq * 64), float("nan"), dtype=torch.float32, device=cuda)
+        err = torch.zeros(1, dtype=torch.int32, device=cuda)
+        lens_d.copy_(torch.from_numpy(lens.astype(np.int32)))  # same pointer every call
+        if plan is None:
+            gkv.decode_layer(dev["qkv"], lens_d, max_len, view, dev["sinks"], out, dev["cos"],
+                             dev["sin"], window=window, workspace=ws_plain, dev_err=err)
+        else:
+            gkv.decode_layer_planned(dev["qkv"], lens_d, max_len, view, dev["sinks"], out,
+                                     dev["cos"], dev["sin"], plan, window=window,
+                                     workspace=ws_plan, dev_err=err)
+        torch.cuda.synchronize()
+        return out, int(err.item())
+
+    lens_d = torch.from_numpy(case.seq_lens.astype(np.int32)).to(cuda)
+    restore()
+    _, err = run(case.seq_lens, gkv.PLAN_KEEP)
+    assert err == 0
+
+    # Move two blocks of two long sequences: swap their contents in both pools
+    # and their table entries, in place. The logical cache is unchanged.
+    tab = case.table
+    b1, b2 = (int(x) for x in np.argsort(-case.seq_lens)[:2])
+    j1, j2 = 0, (int(case.seq_lens[b2]) - 1) % (window or 1 << 30) // 16
+    p1, p2 = int(tab[b1, j1]), int(tab[b2, j2])
+    assert p1 != p2 and p1 >= 0 and p2 >= 0
+    for arr in (dev["k"], dev["v"], snap[0], snap[1]):
+        arr[[p1, p2]] = arr[[p2, p1]]
+    dev["table"][b1, j1] = p2
+    dev["table"][b2, j2] = p1
+    restore()
+    out_r, err_r = run(case.seq_lens, gkv.PLAN_REUSE)
+    assert err_r == 0, f"dev_err {err_r}"
+    bad, worst = allclose_report(out_r.cpu().numpy().reshape(B, -1),
+                                 case.oracle_out().reshape(B, -1), 2e-3, 1e-2)
+    assert bad == 0, f"reuse after a moved block: {bad} outputs off (max err {worst:.3e})"
+    restore()
+    out_p, _ = run(case.seq_lens)
+    assert np.array_equal(_bits(out_r), _bits(out_p))
+
+    # One length changes behind the same pointer: the reuse plans afresh.
+    lens2 = case.seq_lens.copy()
+    lens2[b1] -= 1
+    restore()
+    out_r2, err_r2 = run(lens2, gkv.PLAN_REUSE)
+    assert err_r2 == gkv.DEVERR_PLAN
+    k_r2, v_r2 = dev["k"].clone(), dev["v"].clone()
+    restore()
+    out_p2, err_p2 = run(lens2)
+    assert err_p2 == 0
+    assert np.array_equal(_bits(out_r2), _bits(out_p2))
+    assert torch.equal(k_r2, dev["k"]) and torch.equal(v_r2, dev["v"])
