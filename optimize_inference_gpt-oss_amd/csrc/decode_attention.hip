@@ -126,9 +126,10 @@ struct DecodeArgs {
   int G;              // query heads per kv head
   int B;
   int n_wg;           // split workgroups launched
-  int fixed_S;        // 0: S = T / n_wg (balanced); > 0: this S
+  int fixed_S;        // 0: n_wg balanced ranges (range_start); > 0: ranges of this S
   int aligned;        // ranges of whole sequences (fused launch only; no partials)
   int32_t *plan;      // [kPlanHeader][cu: B + 1][boundary sequence: one per range]
+                      // [range start: one per range, then T]
   int32_t *flat;      // block id of every 16-token block of the stream, per range:
                       // [range][kIdSlab], block k of range w at w * kIdSlab + k
   int32_t *steps;     // step record of every 32-token step: [range][kInfoSlab]
@@ -155,6 +156,29 @@ __device__ __forceinline__ int seq_tokens(const DecodeArgs &a, int b, bool *over
 }
 
 __device__ __forceinline__ int pad_step(int n) { return (n + kStep - 1) & ~(kStep - 1); }
+
+// The ranges of the stream (T tokens, whole steps of 32). S > 0: range k is
+// [k S, (k + 1) S) (a forced split size); S = 0: the n ranges split the T / 32
+// steps as evenly as whole steps allow, range k starting at step
+// floor(k N / n), N = T / 32, so that no workgroup holds a range one step
+// longer than another's plus one (a balanced S rounded up to a step would
+// leave the last range short and its workgroup idle).
+__device__ __forceinline__ int range_start(int k, int T, int S, int n) {
+  if (S > 0)
+    return min((int64_t)k * S, (int64_t)T);
+  if (k >= n)
+    return T;
+  return (int)((int64_t)k * (T / kStep) / n) * kStep;
+}
+
+// The range holding stream position p (0 <= p < T): the last k with
+// range_start(k) <= p.
+__device__ __forceinline__ int range_of(int p, int T, int S, int n) {
+  if (S > 0)
+    return p / S;
+  const int64_t q = p / kStep;
+  return (int)(((q + 1) * n - 1) / (T / kStep));
+}
 
 __device__ __forceinline__ void store_out(void *out, int64_t idx, float v, int is_bf16) {
   if (is_bf16)
@@ -296,9 +320,7 @@ __device__ __forceinline__ void prep_blocks(const DecodeArgs &a, int wg, int n_w
     s_cu[B] = total;
   __syncthreads();
   const int T = s_cu[B];
-  int S = a.fixed_S;
-  if (S == 0)
-    S = max(kStep, pad_step((T + a.n_wg - 1) / a.n_wg));
+  const int S = a.fixed_S, n_r = a.n_wg;
   if (wg == 0) {
     int32_t *cu = a.plan + kPlanHeader;
     for (int b = t; b <= B; b += kPrepThreads)
@@ -306,14 +328,14 @@ __device__ __forceinline__ void prep_blocks(const DecodeArgs &a, int wg, int n_w
     if (t == 0) {
       a.plan[0] = T;
       a.plan[1] = S;
-      a.plan[2] = min(a.n_wg, (T + S - 1) / S);
+      a.plan[2] = n_r;
       a.plan[3] = 0;
       if (a.kept)
         a.kept[0] = 0; // a kept plan is valid until a launch plans afresh
     }
     // per range, the sequence it starts inside of (-1: none), for the combine
     for (int w = t; w < a.n_wg; w += kPrepThreads) {
-      const int tok = w * S;
+      const int tok = range_start(w, T, S, n_r);
       int v = -1;
       if (tok < T) {
         int lo = 0, hi = B - 1; // the last b with cu[b] <= tok
@@ -328,6 +350,8 @@ __device__ __forceinline__ void prep_blocks(const DecodeArgs &a, int wg, int n_w
       }
       a.plan[kPlanHeader + B + 1 + w] = v;
     }
+    for (int w = t; w <= a.n_wg; w += kPrepThreads)
+      a.plan[kPlanHeader + B + 1 + a.n_wg + w] = range_start(w, T, S, n_r);
   }
   // sequences without tokens: output 0
   {
@@ -362,10 +386,11 @@ __device__ __forceinline__ void prep_blocks(const DecodeArgs &a, int wg, int n_w
         any_bad = true;
       }
     }
-    const int w = tok / S; // the range, and the block's place in its slab
-    a.flat[w * kIdSlab + (tok - w * S) / kBlockTokens] = id;
+    const int w = range_of(tok, T, S, n_r); // the range, and the block's place in its slab
+    const int in_r = tok - range_start(w, T, S, n_r);
+    a.flat[w * kIdSlab + in_r / kBlockTokens] = id;
     if ((e & 1) == 0)
-      a.steps[w * kInfoSlab + (tok - w * S) / kStep] =
+      a.steps[w * kInfoSlab + in_r / kStep] =
           step_record(b, off == 0, tok + kStep == s_cu[b + 1], min(max(n - off, 0), kStep));
   }
   if (any_bad && a.dev_err)
@@ -478,6 +503,10 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
     rc = uniform(s_rec[step]);
     // a bad id masks its block like padding (bit jt per block)
     bb = (p0 == kBadBlock ? 1 : 0) | (p1 == kBadBlock ? 2 : 0) | (pass << 2);
+    // a bad id, or a step's missing second block (padding), reads nothing:
+    // its buffer resource covers 0 bytes, so its loads return zeros (masked
+    // anyway) without a memory access
+    const int n0 = p0 >= 0 ? 2048 : 0, n1 = p1 >= 0 ? 2048 : 0;
     p0 = max(p0, 0);
     p1 = max(p1, 0);
     if (KF8) {
@@ -486,12 +515,12 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
       // the 4 scales of tokens 4kg .. 4kg+3 for K and for V
       const size_t c0 = ((size_t)p0 * a.n_kv_heads + g) * (head_bytes / 2);
       const size_t c1 = ((size_t)p1 * a.n_kv_heads + g) * (head_bytes / 2);
-      const __amdgpu_buffer_rsrc_t k0 = head_rsrc((const char *)a.kc + c0);
-      const __amdgpu_buffer_rsrc_t k1 = head_rsrc((const char *)a.kc + c1);
-      const __amdgpu_buffer_rsrc_t v0 = head_rsrc((const char *)a.vc + c0);
-      const __amdgpu_buffer_rsrc_t v1 = head_rsrc((const char *)a.vc + c1);
-      const __amdgpu_buffer_rsrc_t s0 = head_rsrc((const char *)a.vs + c0 / 8);
-      const __amdgpu_buffer_rsrc_t s1 = head_rsrc((const char *)a.vs + c1 / 8);
+      const __amdgpu_buffer_rsrc_t k0 = head_rsrc((const char *)a.kc + c0, n0);
+      const __amdgpu_buffer_rsrc_t k1 = head_rsrc((const char *)a.kc + c1, n1);
+      const __amdgpu_buffer_rsrc_t v0 = head_rsrc((const char *)a.vc + c0, n0);
+      const __amdgpu_buffer_rsrc_t v1 = head_rsrc((const char *)a.vc + c1, n1);
+      const __amdgpu_buffer_rsrc_t s0 = head_rsrc((const char *)a.vs + c0 / 8, n0);
+      const __amdgpu_buffer_rsrc_t s1 = head_rsrc((const char *)a.vs + c1 / 8, n1);
       kr[0] = __builtin_amdgcn_raw_buffer_load_b128(k0, kv_off, 0, kKvAux);
       kr[1] = __builtin_amdgcn_raw_buffer_load_b128(k1, kv_off, 0, kKvAux);
       kr[2] = __builtin_amdgcn_raw_buffer_load_b128(s0, 16 * kg, 0, kKvAux);
@@ -503,10 +532,10 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
     } else {
     const size_t h0 = ((size_t)p0 * a.n_kv_heads + g) * head_bytes;
     const size_t h1 = ((size_t)p1 * a.n_kv_heads + g) * head_bytes;
-    const __amdgpu_buffer_rsrc_t k0 = head_rsrc((const char *)a.kc + h0);
-    const __amdgpu_buffer_rsrc_t k1 = head_rsrc((const char *)a.kc + h1);
-    const __amdgpu_buffer_rsrc_t v0 = head_rsrc((const char *)a.vc + h0);
-    const __amdgpu_buffer_rsrc_t v1 = head_rsrc((const char *)a.vc + h1);
+    const __amdgpu_buffer_rsrc_t k0 = head_rsrc((const char *)a.kc + h0, n0);
+    const __amdgpu_buffer_rsrc_t k1 = head_rsrc((const char *)a.kc + h1, n1);
+    const __amdgpu_buffer_rsrc_t v0 = head_rsrc((const char *)a.vc + h0, n0);
+    const __amdgpu_buffer_rsrc_t v1 = head_rsrc((const char *)a.vc + h1, n1);
     kr[0] = __builtin_amdgcn_raw_buffer_load_b128(k0, kv_off, 0, kKvAux);
     kr[1] = __builtin_amdgcn_raw_buffer_load_b128(k0, kv_off + 1024, 0, kKvAux);
     kr[2] = __builtin_amdgcn_raw_buffer_load_b128(k1, kv_off, 0, kKvAux);
@@ -516,10 +545,10 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
       // 4kg..4kg+3), then the 4 scales of those tokens per block
       const size_t q0 = ((size_t)p0 * a.n_kv_heads + g) * (head_bytes / 2);
       const size_t q1 = ((size_t)p1 * a.n_kv_heads + g) * (head_bytes / 2);
-      const __amdgpu_buffer_rsrc_t c0 = head_rsrc((const char *)a.vc + q0);
-      const __amdgpu_buffer_rsrc_t c1 = head_rsrc((const char *)a.vc + q1);
-      const __amdgpu_buffer_rsrc_t s0 = head_rsrc((const char *)a.vs + q0 / 16);
-      const __amdgpu_buffer_rsrc_t s1 = head_rsrc((const char *)a.vs + q1 / 16);
+      const __amdgpu_buffer_rsrc_t c0 = head_rsrc((const char *)a.vc + q0, n0);
+      const __amdgpu_buffer_rsrc_t c1 = head_rsrc((const char *)a.vc + q1, n1);
+      const __amdgpu_buffer_rsrc_t s0 = head_rsrc((const char *)a.vs + q0 / 16, n0);
+      const __amdgpu_buffer_rsrc_t s1 = head_rsrc((const char *)a.vs + q1 / 16, n1);
       vr[0] = __builtin_amdgcn_raw_buffer_load_b128(c0, vq_off, 0, kKvAux);
       vr[1] = __builtin_amdgcn_raw_buffer_load_b128(c1, vq_off, 0, kKvAux);
       vr[2] = __builtin_amdgcn_raw_buffer_load_b128(s0, 16 * kg, 0, kKvAux);
@@ -903,12 +932,12 @@ void decode_split_kernel(DecodeArgs a) {
     for (int i = threadIdx.x; i < kInfoSlab / 4; i += blockDim.x)
       drec[i] = srec[i];
   }
-  const int T = a.plan[0], S = a.plan[1];
+  const int T = a.plan[0], S = a.plan[1], n_r = a.plan[2];
   __syncthreads();
-  const int rs = w_id * S;
-  if (rs >= T)
+  const int rs = range_start(w_id, T, S, n_r);
+  const int re = range_start(w_id + 1, T, S, n_r);
+  if (rs >= re)
     return;
-  const int re = min(rs + S, T);
   stream_range<R, VF, false>(a, w_id, s_ids, s_rec, nullptr, (re - rs) / kStep);
 }
 
@@ -993,10 +1022,10 @@ __device__ __forceinline__ int plan_key(const DecodeArgs &a, int i, uint2 lh) {
 // bytes per sequence). It then builds the step records and block ids of its
 // own range only, appends the new tokens that fall in its range (one wave per
 // token, all kv heads) and streams the range, the query of each segment
-// coming raw through the load ring. The appends' stores complete before the
-// workgroup barrier that precedes the stream, so every wave of the workgroup
-// reads the new tokens back; no other workgroup reads them (each step of the
-// stream belongs to one range). Workgroup 0 publishes the plan for the
+// coming raw through the load ring. The appends' stores are ordered before
+// the stream's loads by the workgroup barrier that precedes the stream, so
+// every wave of the workgroup reads the new tokens back; no other workgroup
+// reads them (each step of the stream belongs to one range). Workgroup 0 publishes the plan for the
 // combine.
 // mode: bit 0 append; kKeepPlan: also keep the plan in the workspace (each
 // range's bounds, table positions and step records, under a key); kReusePlan:
@@ -1104,7 +1133,7 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
       s_cu[B] = total;
     __syncthreads();
     const int T = s_cu[B];
-    const int S = a.fixed_S > 0 ? a.fixed_S : max(kStep, pad_step((T + a.n_wg - 1) / a.n_wg));
+    const int S = a.fixed_S;
     if (w_id == 0) {
       int32_t *cu = a.plan + kPlanHeader;
       for (int b = t; b <= B; b += nt)
@@ -1112,9 +1141,12 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
       if (t == 0) {
         a.plan[0] = T;
         a.plan[1] = S;
-        a.plan[2] = min(a.n_wg, (T + S - 1) / S);
+        a.plan[2] = a.n_wg;
         a.plan[3] = a.aligned;
       }
+      // each range's first stream position (and the end), for the combine
+      for (int k = t; k <= a.n_wg; k += nt)
+        a.plan[kPlanHeader + B + 1 + a.n_wg + k] = range_start(k, T, S, a.n_wg);
       // a kept plan is valid until a launch plans afresh on this workspace
       if (a.kept) {
         if (keep) {
@@ -1177,13 +1209,15 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
           for (int i = t; i < n_out; i += nt)
             store_out(a.out, (int64_t)b * a.out_stride + i, 0.0f, a.out_bf16);
     } else {
-      rs = min(w_id * S, T);
-      re = min(rs + S, T);
+      rs = range_start(w_id, T, S, a.n_wg);
+      re = range_start(w_id + 1, T, S, a.n_wg);
     }
     // The sequences that overlap the range, a run of consecutive indices:
     // from the one holding position rs (the last b with cu[b] <= rs) to the
-    // last one starting before re.
-    if (rs < re) {
+    // last one starting before re. (The first is found for a range without
+    // tokens too, when rs < T: the combine needs the sequence that every
+    // range, empty or not, starts inside of.)
+    if (rs < T) {
       int lo = 0, hi = B - 1;
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -1193,7 +1227,9 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
           hi = mid - 1;
       }
       b_first = lo;
-      hi = B; // the first b with cu[b] >= re (cu[B] = T >= re)
+    }
+    if (rs < re) {
+      int lo = b_first, hi = B; // the first b with cu[b] >= re (cu[B] = T >= re)
       while (lo < hi) {
         const int mid = (lo + hi) >> 1;
         if (s_cu[mid] >= re)
@@ -1210,7 +1246,7 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
       // launched per range boundary; and the sequences without tokens
       // (output 0), written by workgroup b % n_wg.
       if (t == 0)
-        a.plan[kPlanHeader + B + 1 + w_id] = rs < re && rs > s_cu[b_first] ? b_first : -1;
+        a.plan[kPlanHeader + B + 1 + w_id] = rs < T && rs > s_cu[b_first] ? b_first : -1;
       const int n_out = a.n_kv_heads * a.G * kHeadDim;
       for (int b = w_id; b < B; b += a.n_wg)
         if (s_cu[b + 1] == s_cu[b])
@@ -1348,11 +1384,11 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
   }
   if (any_bad && a.dev_err)
     atomicOr(a.dev_err, GKV_DEVERR_BLOCK_ID);
-  // The appends' stores complete, then the barrier: the waves of this
-  // workgroup share one CU and its caches, so every wave then reads the new
-  // tokens back.
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8)); // vmcnt(0)
+  // The barrier orders the appends' stores before every wave's stream loads:
+  // the waves of a workgroup share one CU, whose vector memory path keeps
+  // their accesses in order, so (as for any write, __syncthreads, read within
+  // a workgroup) the new tokens are read back without waiting for the stores
+  // to complete.
   __syncthreads();
 
   // The stream reads its arguments afresh from the kernel-argument segment
@@ -1371,41 +1407,45 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
 // Sequence b's output from its partials, one wave per kv head g; lane (h =
 // lane / 8) merges dims 8*(lane % 8) .. +7 of query head h over them:
 // M = max(sink, m_w), L = 2^(sink-M) + sum l_w 2^(m_w-M), out = sum o_w 2^(m_w-M) / L
-// (the merge of fast_attention.hpp:403-424, across workgroups). Returns at
-// once if the sequence lies in one range (finished by its split workgroup).
-__device__ __forceinline__ void combine_sequence(const DecodeArgs &a, int b) {
+// (the merge of fast_attention.hpp:403-424, across workgroups). w is the
+// first range that starts inside b: b starts in range w - 1 and its pieces
+// are in ranges w - 1 .. w1, the last range that starts inside it (read from
+// the per-range table, so no range is computed here).
+__device__ __forceinline__ void combine_sequence(const DecodeArgs &a, int b, int w) {
   constexpr int D = kHeadDim;
   const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, h = lane >> 3, d0 = 8 * (lane & 7);
   if (h >= a.G)
     return;
   const int32_t *cu = a.plan + kPlanHeader;
-  const int S = a.plan[1];
-  const int c0 = cu[b], c1 = cu[b + 1];
+  const int32_t *bnd = cu + a.B + 1;     // per range: the sequence it starts inside of
+  const int32_t *rsa = bnd + a.n_wg;     // per range: its first stream position (+ end)
+  const int w0 = w - 1;
+  int w1 = w;
+  while (w1 + 1 < a.n_wg && bnd[w1 + 1] == b)
+    w1++;
+  const int c0 = cu[b];
   const int64_t ob = (int64_t)b * a.out_stride + (int64_t)(g * a.G + h) * D + d0;
-  if (c1 == c0) { // no tokens: all weight on the sink
-    for (int i = 0; i < 8; i++)
-      store_out(a.out, ob + i, 0.0f, a.out_bf16);
-    return;
-  }
-  const int w0 = c0 / S, w1 = (c1 - 1) / S;
-  if (w0 == w1)
-    return; // finished by its split workgroup
   const float sk = a.sinks[g * a.G + h] * kLog2e;
   // the sequence's piece in range w: that range's last segment (slot 1) for
   // the first range unless the sequence starts exactly there, else its
-  // first segment (slot 0)
-  auto part_of = [&](int w) -> int64_t {
-    const int slot = (w == w0 && c0 != w0 * S) ? 1 : 0;
-    return ((int64_t)w * kPartsPerRange + slot) * a.n_kv_heads + g;
+  // first segment (slot 0); ranges without tokens (possible when there are
+  // fewer steps than ranges) hold no piece
+  auto part_of = [&](int r) -> int64_t {
+    const int slot = (r == w0 && c0 != rsa[w0]) ? 1 : 0;
+    return ((int64_t)r * kPartsPerRange + slot) * a.n_kv_heads + g;
   };
+  auto empty = [&](int r) -> bool { return rsa[r] == rsa[r + 1]; };
   float M = sk;
-  for (int w = w0; w <= w1; w++)
-    M = fmaxf(M, a.ws_ml[part_of(w) * kMlStride + 2 * h]);
+  for (int r = w0; r <= w1; r++)
+    if (!empty(r))
+      M = fmaxf(M, a.ws_ml[part_of(r) * kMlStride + 2 * h]);
   float Ls = __builtin_amdgcn_exp2f(sk - M);
   f32x4 o0 = {0, 0, 0, 0}, o1 = {0, 0, 0, 0};
-  for (int w = w0; w <= w1; w++) {
-    const int64_t part = part_of(w);
+  for (int r = w0; r <= w1; r++) {
+    if (empty(r))
+      continue;
+    const int64_t part = part_of(r);
     const float c = __builtin_amdgcn_exp2f(a.ws_ml[part * kMlStride + 2 * h] - M);
     Ls = fmaf(a.ws_ml[part * kMlStride + 2 * h + 1], c, Ls);
     const f32x4 *po = (const f32x4 *)(a.ws_o + part * kPartFloats + h * D + d0);
@@ -1432,7 +1472,7 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
   const int b = bnd[w];
   if (b < 0 || (w > 0 && bnd[w - 1] == b))
     return;
-  combine_sequence(a, b);
+  combine_sequence(a, b, w);
 }
 
 // ---- host side --------------------------------------------------------------------
@@ -1506,7 +1546,7 @@ struct WorkspaceLayout {
 static WorkspaceLayout layout_of(int B, int n_kv_heads, int max_wg) {
   WorkspaceLayout L;
   L.plan = 0;
-  L.ws_o = align256((size_t)(kPlanHeader + B + 1 + max_wg) * 4);
+  L.ws_o = align256((size_t)(kPlanHeader + B + 1 + 2 * max_wg + 1) * 4);
   const size_t parts = (size_t)kPartsPerRange * max_wg * n_kv_heads;
   L.ws_ml = L.ws_o + parts * kPartFloats * sizeof(float);
   L.flat = align256(L.ws_ml + parts * kMlStride * sizeof(float));
@@ -1929,7 +1969,8 @@ extern "C" int gkv_decode_layer_split_planned(GKV_LAYER_PARAMS, int32_t plan) {
 namespace gkv {
 constexpr int kScratchWorkgroups = 512; // ranges (split workgroups) the scratch holds
 constexpr size_t kScratchBytes =
-    ((((size_t)(kPlanHeader + kMaxBatch + 1 + kScratchWorkgroups) * 4 + 255) & ~(size_t)255) +
+    ((((size_t)(kPlanHeader + kMaxBatch + 1 + 2 * kScratchWorkgroups + 1) * 4 + 255) &
+      ~(size_t)255) +
      (size_t)kPartsPerRange * kScratchWorkgroups * 8 * (kPartFloats + kMlStride) * 4 + 255) &
     ~(size_t)255;
 static __device__ __align__(256) char scratch[kScratchBytes];

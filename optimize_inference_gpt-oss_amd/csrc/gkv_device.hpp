@@ -21,8 +21,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // Buffer resource over the 2 KB of one head of one paged block: loads take a
 // scalar base and a 32-bit per-lane offset; reads past 2 KB return zero.
 // Word 3 = 0x00020000: 32-bit data format, the gfx9-family raw-buffer setting.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const void *base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 2048, 0x00020000);
+// bytes = 0: every load through it returns zeros without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const void *base, int bytes = 2048) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, bytes, 0x00020000);
 }
 
 // fp32 -> bf16 bits, round to nearest even, NaN kept quiet. Written out in

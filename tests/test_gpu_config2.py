@@ -56,13 +56,15 @@ def test_config2_full_batch(gkv, cuda, torch_mod):
         # sequences of the sample that the ranges cut (their pieces merged by
         # the combine): stream offsets from the padded lengths, S from the plan
         plan = ws[:16].view(torch.int32).cpu().numpy()
-        T, S = int(plan[0]), int(plan[1])
+        T, S, n_r = int(plan[0]), int(plan[1]), int(plan[2])
         n = (P.seq_lens + 31) // 32 * 32
         cu = np.concatenate([[0], np.cumsum(n)])
-        assert T == cu[-1]
-        cut = [b for b in sample if cu[b] // S != (cu[b + 1] - 1) // S]
-        print(f"range size {S} tokens; {len(cut)} of {len(sample)} sampled sequences cut",
-              flush=True)
+        assert T == cu[-1] and S == 0  # balanced ranges: range k starts at step k N / n_r
+        starts = np.array([k * (T // 32) // n_r * 32 for k in range(n_r)])
+        range_of = lambda p: int(np.searchsorted(starts, p, side="right")) - 1  # noqa: E731
+        cut = [b for b in sample if range_of(cu[b]) != range_of(cu[b + 1] - 1)]
+        print(f"{n_r} ranges of ~{T // n_r} tokens; {len(cut)} of {len(sample)} sampled "
+              "sequences cut", flush=True)
         assert len(cut) >= 20
         got = out.cpu().numpy().reshape(B, 64, 64)[sample]
         ref = P.oracle_out(0, k1, v1, sample)
