@@ -639,6 +639,9 @@ def main() -> int:
     ap.add_argument("--qkv-rows", type=int, default=0,
                     help="rows of the --qkv-projection run (default: config 2's 512 decode rows; "
                          "config 4's prompts hold 19024)")
+    ap.add_argument("--settle-s", type=float, default=0.2,
+                    help="untimed steps for this many seconds before the warmup steps (the "
+                         "GPU leaves the setup at idle clocks)")
     ap.add_argument("--yardstick", action="store_true",
                     help="ceiling yardsticks: a plain read and a random 2 KB-block gather of "
                          "the layer's K/V bytes, and the decode launch with loads only, next "
@@ -774,6 +777,16 @@ def main() -> int:
                 e[-1].record(stream)
                 ev.setdefault(li, []).append(e)
 
+    # Settle: the GPU comes out of the host-side setup (pool fill, inputs) at
+    # idle clocks; untimed steps for --settle-s seconds bring it to the clocks
+    # it keeps under a steady decode load, before the W warmup steps.
+    settle_steps = 0
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < args.settle_s:
+        for _ in range(10):
+            step(False)
+        settle_steps += 10
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         step(False)
     torch.cuda.synchronize()
@@ -857,6 +870,7 @@ def main() -> int:
             "plan": "kept by each kind's first layer, reused by the others"
                     if plan_of[-1] is not None else "every layer plans",
             "kernel_ms": dict(zip(stages, (round(float(x), 4) for x in stage_ms))),
+            "settle": f"{settle_steps} untimed steps ({args.settle_s} s) before the warmup",
             "parallelism": "1 GPU",
         },
         "roofline": {

@@ -137,6 +137,8 @@ struct DecodeArgs {
   int32_t *kept;      // kept plan: [kKeyInts] key, then int4 {rs, re, b_first, n_seq} per range
   float *ws_o;        // [range][kPartsPerRange][Hkv][8][64]: partial outputs
   float *ws_ml;       // [range][kPartsPerRange][Hkv][8][2]: their (m, l)
+  int4 *crec;         // [range]: the combine's record ({b, w0, w1, cu[b]} of the sequence the
+                      // range is the first to start inside of; b = -1: none)
   void *out;
   int64_t out_stride;
   int out_bf16;
@@ -206,6 +208,17 @@ __device__ __forceinline__ u32x2 int8x4_to_bf16x4(uint32_t w) {
     h[i] = __float_as_uint((float)c) >> 16;
   }
   return u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+}
+
+// The combine's record for range w, which starts at stream position rs and
+// inside sequence b ([c0, c1) of the stream; b = -1: at a sequence's start or
+// past the stream): the sequence's pieces are in ranges w0 = w - 1 .. w1,
+// and range w merges them if it is the first range to start inside it.
+__device__ __forceinline__ int4 combine_record(int w, int b, int c0, int c1, int T, int S,
+                                               int n) {
+  if (b < 0 || w == 0 || range_start(w - 1, T, S, n) > c0)
+    return int4{-1, 0, 0, 0};
+  return int4{b, w - 1, range_of(c1 - 1, T, S, n), c0};
 }
 
 // ---- prep -----------------------------------------------------------------------
@@ -349,6 +362,7 @@ __device__ __forceinline__ void prep_blocks(const DecodeArgs &a, int wg, int n_w
         v = tok > s_cu[lo] ? lo : -1;
       }
       a.plan[kPlanHeader + B + 1 + w] = v;
+      a.crec[w] = combine_record(w, v, v >= 0 ? s_cu[v] : 0, v >= 0 ? s_cu[v + 1] : 0, T, S, n_r);
     }
     for (int w = t; w <= a.n_wg; w += kPrepThreads)
       a.plan[kPlanHeader + B + 1 + a.n_wg + w] = range_start(w, T, S, n_r);
@@ -1241,12 +1255,18 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
     }
     if (keep && t == 0)
       kept_ranges[w_id] = int4{rs, max(re, rs), b_first, n_seq};
+    if (a.aligned && t == 0)
+      a.crec[w_id] = int4{-1, 0, 0, 0}; // whole sequences: nothing to combine
     if (!a.aligned) {
       // The sequence this range starts inside of (-1: none), for the combine
       // launched per range boundary; and the sequences without tokens
       // (output 0), written by workgroup b % n_wg.
-      if (t == 0)
-        a.plan[kPlanHeader + B + 1 + w_id] = rs < T && rs > s_cu[b_first] ? b_first : -1;
+      if (t == 0) {
+        const int v = rs < T && rs > s_cu[b_first] ? b_first : -1;
+        a.plan[kPlanHeader + B + 1 + w_id] = v;
+        a.crec[w_id] = combine_record(w_id, v, v >= 0 ? s_cu[v] : 0, v >= 0 ? s_cu[v + 1] : 0, T,
+                                      S, a.n_wg);
+      }
       const int n_out = a.n_kv_heads * a.G * kHeadDim;
       for (int b = w_id; b < B; b += a.n_wg)
         if (s_cu[b + 1] == s_cu[b])
@@ -1404,75 +1424,98 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
 
 // ---- combine --------------------------------------------------------------------
 
-// Sequence b's output from its partials, one wave per kv head g; lane (h =
-// lane / 8) merges dims 8*(lane % 8) .. +7 of query head h over them:
+// Sequence b's output from its pieces in ranges w0 .. w1 (the stream
+// positions [c0, c1) meet them), one wave per kv head g; lane (h = lane / 8)
+// merges dims 8*(lane % 8) .. +7 of query head h:
 // M = max(sink, m_w), L = 2^(sink-M) + sum l_w 2^(m_w-M), out = sum o_w 2^(m_w-M) / L
-// (the merge of fast_attention.hpp:403-424, across workgroups). w is the
-// first range that starts inside b: b starts in range w - 1 and its pieces
-// are in ranges w - 1 .. w1, the last range that starts inside it (read from
-// the per-range table, so no range is computed here).
-__device__ __forceinline__ void combine_sequence(const DecodeArgs &a, int b, int w) {
+// (the merge of fast_attention.hpp:403-424, across workgroups). The piece in
+// range w is that range's last segment (slot 1) for the first range unless
+// the sequence starts exactly there, else its first segment (slot 0); ranges
+// without tokens (possible when there are fewer steps than ranges) hold none.
+// Up to kCombineAtOnce ranges, every load goes out at once (one round trip).
+constexpr int kCombineAtOnce = 4;
+__device__ __forceinline__ void combine_sequence(const DecodeArgs &a, int4 rec) {
   constexpr int D = kHeadDim;
   const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, h = lane >> 3, d0 = 8 * (lane & 7);
   if (h >= a.G)
     return;
-  const int32_t *cu = a.plan + kPlanHeader;
-  const int32_t *bnd = cu + a.B + 1;     // per range: the sequence it starts inside of
-  const int32_t *rsa = bnd + a.n_wg;     // per range: its first stream position (+ end)
-  const int w0 = w - 1;
-  int w1 = w;
-  while (w1 + 1 < a.n_wg && bnd[w1 + 1] == b)
-    w1++;
-  const int c0 = cu[b];
-  const int64_t ob = (int64_t)b * a.out_stride + (int64_t)(g * a.G + h) * D + d0;
-  const float sk = a.sinks[g * a.G + h] * kLog2e;
-  // the sequence's piece in range w: that range's last segment (slot 1) for
-  // the first range unless the sequence starts exactly there, else its
-  // first segment (slot 0); ranges without tokens (possible when there are
-  // fewer steps than ranges) hold no piece
-  auto part_of = [&](int r) -> int64_t {
-    const int slot = (r == w0 && c0 != rsa[w0]) ? 1 : 0;
+  const int b = rec.x, w0 = rec.y, w1 = rec.z, c0 = rec.w;
+  const int32_t *rsa = a.plan + kPlanHeader + a.B + 1 + a.n_wg; // range starts (+ the end)
+  auto part_of = [&](int r, int rs) -> int64_t {
+    const int slot = (r == w0 && c0 != rs) ? 1 : 0;
     return ((int64_t)r * kPartsPerRange + slot) * a.n_kv_heads + g;
   };
-  auto empty = [&](int r) -> bool { return rsa[r] == rsa[r + 1]; };
-  float M = sk;
-  for (int r = w0; r <= w1; r++)
-    if (!empty(r))
-      M = fmaxf(M, a.ws_ml[part_of(r) * kMlStride + 2 * h]);
-  float Ls = __builtin_amdgcn_exp2f(sk - M);
+  const int64_t ob = (int64_t)b * a.out_stride + (int64_t)(g * a.G + h) * D + d0;
+  const float sk = a.sinks[g * a.G + h] * kLog2e;
+  float M = sk, Ls, inv;
   f32x4 o0 = {0, 0, 0, 0}, o1 = {0, 0, 0, 0};
-  for (int r = w0; r <= w1; r++) {
-    if (empty(r))
-      continue;
-    const int64_t part = part_of(r);
-    const float c = __builtin_amdgcn_exp2f(a.ws_ml[part * kMlStride + 2 * h] - M);
-    Ls = fmaf(a.ws_ml[part * kMlStride + 2 * h + 1], c, Ls);
-    const f32x4 *po = (const f32x4 *)(a.ws_o + part * kPartFloats + h * D + d0);
-    o0 += po[0] * c;
-    o1 += po[1] * c;
+  if (w1 - w0 < kCombineAtOnce) {
+    float m[kCombineAtOnce], l[kCombineAtOnce];
+    f32x4 pa[kCombineAtOnce], pb[kCombineAtOnce];
+    bool ok[kCombineAtOnce];
+#pragma unroll
+    for (int i = 0; i < kCombineAtOnce; i++) {
+      const int r = w0 + i;
+      ok[i] = false;
+      if (r <= w1) {
+        const int rs = rsa[r];
+        ok[i] = rs != rsa[r + 1];
+        const int64_t part = part_of(r, rs);
+        m[i] = a.ws_ml[part * kMlStride + 2 * h];
+        l[i] = a.ws_ml[part * kMlStride + 2 * h + 1];
+        const f32x4 *po = (const f32x4 *)(a.ws_o + part * kPartFloats + h * D + d0);
+        pa[i] = po[0];
+        pb[i] = po[1];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kCombineAtOnce; i++)
+      if (ok[i])
+        M = fmaxf(M, m[i]);
+    Ls = __builtin_amdgcn_exp2f(sk - M);
+#pragma unroll
+    for (int i = 0; i < kCombineAtOnce; i++)
+      if (ok[i]) {
+        const float c = __builtin_amdgcn_exp2f(m[i] - M);
+        Ls = fmaf(l[i], c, Ls);
+        o0 += pa[i] * c;
+        o1 += pb[i] * c;
+      }
+  } else {
+    for (int r = w0; r <= w1; r++)
+      if (rsa[r] != rsa[r + 1])
+        M = fmaxf(M, a.ws_ml[part_of(r, rsa[r]) * kMlStride + 2 * h]);
+    Ls = __builtin_amdgcn_exp2f(sk - M);
+    for (int r = w0; r <= w1; r++) {
+      if (rsa[r] == rsa[r + 1])
+        continue;
+      const int64_t part = part_of(r, rsa[r]);
+      const float c = __builtin_amdgcn_exp2f(a.ws_ml[part * kMlStride + 2 * h] - M);
+      Ls = fmaf(a.ws_ml[part * kMlStride + 2 * h + 1], c, Ls);
+      const f32x4 *po = (const f32x4 *)(a.ws_o + part * kPartFloats + h * D + d0);
+      o0 += po[0] * c;
+      o1 += po[1] * c;
+    }
   }
-  const float inv = 1.0f / Ls;
+  inv = 1.0f / Ls;
   for (int i = 0; i < 4; i++) {
     store_out(a.out, ob + i, o0[i] * inv, a.out_bf16);
     store_out(a.out, ob + 4 + i, o1[i] * inv, a.out_bf16);
   }
 }
 
-// One workgroup per range: the split launches (or the prepare launch of the
-// staged ones) have written the outputs of sequences without tokens and, per
-// range, the sequence the range starts inside of; range w merges that
-// sequence unless an earlier range starts inside it too. n_wg workgroups
-// instead of one per sequence, most of them returning at once.
+// One workgroup per range, a wave per kv head: the split launch (or the
+// prepare launch of the staged ones) left, per range, the record of the
+// sequence the range is the first to start inside of (its pieces' ranges and
+// stream start), so the merge is two round trips: the record, then every
+// piece at once. n_wg workgroups instead of one per sequence, most of them
+// returning at once.
 __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
-  if (a.plan[3])
+  const int4 rec = a.crec[blockIdx.x];
+  if (rec.x < 0)
     return;
-  const int w = blockIdx.x;
-  const int32_t *bnd = a.plan + kPlanHeader + a.B + 1;
-  const int b = bnd[w];
-  if (b < 0 || (w > 0 && bnd[w - 1] == b))
-    return;
-  combine_sequence(a, b, w);
+  combine_sequence(a, rec);
 }
 
 // ---- host side --------------------------------------------------------------------
@@ -1533,20 +1576,21 @@ static int resident_workgroups(int n_kv_heads) {
   return slot;
 }
 
-static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+static constexpr size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Workspace layout: plan | partials (o) | partials (m, l) | then, for the
 // staged launches and the kept plan only: block ids | step records | query
 // operands | kept plan. The split that plans in its prologue uses the first
 // three (fused_total bytes).
 struct WorkspaceLayout {
-  size_t plan, ws_o, ws_ml, flat, steps, qops, kept, fused_total, total;
+  size_t plan, crec, ws_o, ws_ml, flat, steps, qops, kept, fused_total, total;
 };
 
-static WorkspaceLayout layout_of(int B, int n_kv_heads, int max_wg) {
-  WorkspaceLayout L;
+static constexpr WorkspaceLayout layout_of(int B, int n_kv_heads, int max_wg) {
+  WorkspaceLayout L{};
   L.plan = 0;
-  L.ws_o = align256((size_t)(kPlanHeader + B + 1 + 2 * max_wg + 1) * 4);
+  L.crec = align256((size_t)(kPlanHeader + B + 1 + 2 * max_wg + 1) * 4);
+  L.ws_o = align256(L.crec + (size_t)max_wg * 16);
   const size_t parts = (size_t)kPartsPerRange * max_wg * n_kv_heads;
   L.ws_ml = L.ws_o + parts * kPartFloats * sizeof(float);
   L.flat = align256(L.ws_ml + parts * kMlStride * sizeof(float));
@@ -1669,6 +1713,7 @@ static int prepare(DecodeArgs &a, int32_t B, int32_t n_q_heads, const float *q, 
   a.qops = (u32x4 *)(ws + L.qops);
   a.kept = staged_parts ? (int32_t *)(ws + L.kept) : nullptr;
   a.ws_o = (float *)(ws + L.ws_o);
+  a.crec = (int4 *)(ws + L.crec);
   a.ws_ml = (float *)(ws + L.ws_ml);
   a.out = out;
   a.out_stride = out_stride;
@@ -1968,11 +2013,7 @@ extern "C" int gkv_decode_layer_split_planned(GKV_LAYER_PARAMS, int32_t plan) {
 
 namespace gkv {
 constexpr int kScratchWorkgroups = 512; // ranges (split workgroups) the scratch holds
-constexpr size_t kScratchBytes =
-    ((((size_t)(kPlanHeader + kMaxBatch + 1 + 2 * kScratchWorkgroups + 1) * 4 + 255) &
-      ~(size_t)255) +
-     (size_t)kPartsPerRange * kScratchWorkgroups * 8 * (kPartFloats + kMlStride) * 4 + 255) &
-    ~(size_t)255;
+constexpr size_t kScratchBytes = layout_of(kMaxBatch, 8, kScratchWorkgroups).fused_total;
 static __device__ __align__(256) char scratch[kScratchBytes];
 constexpr int kMaxDevices = 64;
 

@@ -193,7 +193,8 @@ def test_layer_combines_argument_checks(gkv):
 
 
 def test_workspace_formula(gkv):
-    # plan (header + prefix sums + one boundary sequence per range); partial results of 2 segments per range for
+    # plan (header + prefix sums + per range the sequence it starts inside of
+    # and its start) and the combine's record per range; partial results of 2 segments per range for
     # up to 1024 ranges, 8 heads x (64 + 2) floats per kv head; then, for the
     # staged launches, block ids (1024 per range) and step records (512 per
     # range: ranges of up to 16384 tokens) and the query operands (2 KB per
@@ -204,7 +205,9 @@ def test_workspace_formula(gkv):
 
     B, hkv = 512, 8
     parts = 2 * 1024 * hkv
-    fused = a256(a256((4 + B + 1 + 1024) * 4) + parts * (512 + 16) * 4)
+    plan = a256((4 + B + 1 + 2 * 1024 + 1) * 4)  # + one range start per range, then T
+    crec = a256(plan + 1024 * 16)                  # the combine's record per range
+    fused = a256(crec + parts * (512 + 16) * 4)
     staged = (a256(1024 * 1024 * 4) + a256(1024 * 512 * 4) + a256(B * hkv * 2048)
               + a256((16 + 4 * 1024) * 4))
     assert gkv.workspace_bytes(B, hkv, 2049) == fused + staged
