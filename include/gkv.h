@@ -381,7 +381,11 @@ int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_seqlens, in
  * paged cache (chunked prefill), same semantics: row j of prompt b is position
  * start_pos[b] + j and attends to positions max(0, p - W + 1) .. p, plus the
  * sink. start_pos: device int32 [B], multiples of 16 (else GKV_DEVERR_ALIGN
- * and the rows attend to themselves only), or NULL (all 0).
+ * is set and that prompt's outputs are meaningless, though finite), or NULL
+ * (all 0). For a full layer (cache.ring = 0) the positions must stay below
+ * cache.table_stride * 16 (the cos/sin tables cover them): a prompt that runs
+ * past sets GKV_DEVERR_LENGTH, and its rows beyond take their angles at the
+ * last position that fits (meaningless outputs, no read past the tables).
  *   keys before start_pos[b]  from the cache (gkv_cache_view in any format:
  *            a quantized K or V stands for value(code) * scale): the full
  *            layer's table, or a ring of W slots (cache.ring == window), which
@@ -390,7 +394,8 @@ int gkv_prefill_attention(void *stream, int32_t B, const int32_t *cu_seqlens, in
  *            gkv_kv_append's k_pack/v_pack of this chunk); k = v = NULL: from
  *            the cache as well (a full layer whose chunk was appended first)
  *   dev_err  NULL, or a device uint32 that gets GKV_DEVERR_* bits (block ids
- *            outside the pool, misaligned start positions, V out of range)
+ *            outside the pool, misaligned start positions, positions past a
+ *            full layer's table, V out of range)
  * The other arguments are gkv_prefill_attention's; cos/sin rows are taken at
  * the rows' positions. */
 int gkv_prefill_paged(void *stream, int32_t B, const int32_t *cu_seqlens,
@@ -429,7 +434,13 @@ int gkv_pool_seq_alloc(gkv_pool *pool, int32_t *seq_id);
 int gkv_pool_seq_reserve(gkv_pool *pool, int32_t seq_id, int32_t seq_len);
 /* Returns the sequence's blocks to the free list. */
 int gkv_pool_seq_free(gkv_pool *pool, int32_t seq_id);
-/* Copies the host block tables to the device (after alloc/reserve/free). */
+/* Brings the device block tables up to date after alloc/reserve/free, on
+ * stream, without waiting: only the entries changed since the last sync go,
+ * from a pinned staging buffer the pool owns (one of two, each reused only
+ * once its copy has completed) through a small scatter kernel, so kernels
+ * queued after it on the same stream see the new tables and the host may
+ * reserve and free again at once. (The pool's creation uploads both tables
+ * whole.) No counterpart in the reference, whose caches are not paged. */
 int gkv_pool_sync(gkv_pool *pool, void *stream);
 /* Cache view of layer l over the table rows of sequence ids 0 .. max_seqs-1
  * (rows of the batch must be sequence ids: pass row_seq or order the batch by id). */

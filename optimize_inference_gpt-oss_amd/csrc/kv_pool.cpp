@@ -11,7 +11,8 @@
 //   window layers  a ring of W/16 blocks per sequence id, fixed at create time
 //                  (the reference's slots = window, gpu_engine.hpp:318-319)
 //   tables         int32 [max_seqs][ceil(max_seq_len/16)] and [max_seqs][W/16],
-//                  mirrored on the host; gkv_pool_sync uploads them
+//                  mirrored on the host; gkv_pool_sync uploads the entries that
+//                  changed since the last sync, without waiting
 // Sizing: num_blocks explicit, or derived from a byte budget, by default 90%
 // of the free device memory (288 GB HBM3E on MI355X), instead of the
 // reference's halve-the-batch-until-it-fits loop (gpu_fit_batch :425-433).
@@ -51,8 +52,37 @@ struct gkv_pool {
   std::vector<char> seq_live;
   std::vector<int32_t> free_seqs;
   int64_t device_bytes = 0;
+  // Incremental sync: the full-table entries changed since the last sync,
+  // as (index, value); they go to the device through one of two pinned
+  // staging buffers (reused only once the copy out of it has completed) and
+  // a scatter kernel. The first sync uploads the whole tables.
+  std::vector<int2> pending;
+  bool whole = true;
+  int2 *h_stage[2] = {nullptr, nullptr};
+  int2 *d_stage[2] = {nullptr, nullptr};
+  hipEvent_t stage_done[2] = {nullptr, nullptr};
+  size_t stage_cap = 0; // entries per staging buffer
+  int stage_i = 0;
+
+  void free_stage() {
+    for (int i = 0; i < 2; i++) {
+      if (stage_done[i]) {
+        (void)hipEventSynchronize(stage_done[i]);
+        (void)hipEventDestroy(stage_done[i]);
+      }
+      if (h_stage[i])
+        (void)hipHostFree(h_stage[i]);
+      if (d_stage[i])
+        (void)hipFree(d_stage[i]);
+      h_stage[i] = nullptr;
+      d_stage[i] = nullptr;
+      stage_done[i] = nullptr;
+    }
+    stage_cap = 0;
+  }
 
   ~gkv_pool() {
+    free_stage();
     for (auto *vec : {&k_full, &v_full, &k_ring, &v_ring, &s_full, &s_ring})
       for (void *p : *vec)
         if (p)
@@ -237,10 +267,12 @@ extern "C" int gkv_pool_seq_reserve(gkv_pool *pool, int32_t seq_id, int32_t seq_
     return GKV_OK;
   if ((int64_t)(need - have) > (int64_t)pool->free_blocks.size())
     return GKV_ERR_CAPACITY; // nothing taken: all or none
-  int32_t *row = &pool->h_table[(size_t)seq_id * pool->table_stride];
+  const size_t base = (size_t)seq_id * pool->table_stride;
+  int32_t *row = &pool->h_table[base];
   for (int32_t j = have; j < need; j++) {
     row[j] = pool->free_blocks.back();
     pool->free_blocks.pop_back();
+    pool->pending.push_back(int2{(int)(base + j), row[j]});
   }
   pool->seq_blocks[seq_id] = need;
   return GKV_OK;
@@ -251,10 +283,12 @@ extern "C" int gkv_pool_seq_free(gkv_pool *pool, int32_t seq_id) {
     return GKV_ERR_ARG;
   if (seq_id < 0 || seq_id >= pool->cfg.max_seqs || !pool->seq_live[seq_id])
     return GKV_ERR_BLOCK;
-  int32_t *row = &pool->h_table[(size_t)seq_id * pool->table_stride];
+  const size_t base = (size_t)seq_id * pool->table_stride;
+  int32_t *row = &pool->h_table[base];
   for (int32_t j = pool->seq_blocks[seq_id] - 1; j >= 0; j--) {
     pool->free_blocks.push_back(row[j]);
     row[j] = -1;
+    pool->pending.push_back(int2{(int)(base + j), -1});
   }
   pool->seq_blocks[seq_id] = 0;
   pool->seq_live[seq_id] = 0;
@@ -262,20 +296,75 @@ extern "C" int gkv_pool_seq_free(gkv_pool *pool, int32_t seq_id) {
   return GKV_OK;
 }
 
+// Applies n staged (index, value) pairs to the device table, in order (a
+// later pair for the same entry wins: each thread takes a distinct pair, and
+// the pairs of one entry never repeat within a sync, see gkv_pool_sync).
+__global__ void pool_scatter_kernel(int32_t *table, const int2 *pairs, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n)
+    table[pairs[i].x] = pairs[i].y;
+}
+
 extern "C" int gkv_pool_sync(gkv_pool *pool, void *stream) {
   if (!pool)
     return GKV_ERR_ARG;
   hipStream_t s = (hipStream_t)stream;
-  if (hipMemcpyAsync(pool->d_table, pool->h_table.data(), pool->h_table.size() * 4,
-                     hipMemcpyHostToDevice, s) != hipSuccess)
+  if (pool->whole) {
+    // the first sync: both tables whole, waited for (create time)
+    if (hipMemcpyAsync(pool->d_table, pool->h_table.data(), pool->h_table.size() * 4,
+                       hipMemcpyHostToDevice, s) != hipSuccess)
+      return GKV_ERR_HIP;
+    if (pool->d_ring_table &&
+        hipMemcpyAsync(pool->d_ring_table, pool->h_ring_table.data(),
+                       pool->h_ring_table.size() * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+      return GKV_ERR_HIP;
+    if (hipStreamSynchronize(s) != hipSuccess)
+      return GKV_ERR_HIP;
+    pool->whole = false;
+    pool->pending.clear();
+    return GKV_OK;
+  }
+  if (pool->pending.empty())
+    return GKV_OK;
+  // One pair per changed entry, its latest value (a reserve after a free of
+  // the same entry within one sync leaves two pairs; the host table holds
+  // the value that counts).
+  std::vector<int2> &pend = pool->pending;
+  std::sort(pend.begin(), pend.end(), [](const int2 &x, const int2 &y) { return x.x < y.x; });
+  pend.erase(std::unique(pend.begin(), pend.end(),
+                         [](const int2 &x, const int2 &y) { return x.x == y.x; }),
+             pend.end());
+  for (int2 &e : pend)
+    e.y = pool->h_table[e.x];
+  const size_t n = pend.size();
+  if (n > pool->stage_cap) {
+    pool->free_stage();
+    const size_t cap = std::max<size_t>(n, 4096);
+    for (int i = 0; i < 2; i++)
+      if (hipHostMalloc((void **)&pool->h_stage[i], cap * sizeof(int2), hipHostMallocDefault) !=
+              hipSuccess ||
+          hipMalloc((void **)&pool->d_stage[i], cap * sizeof(int2)) != hipSuccess ||
+          hipEventCreateWithFlags(&pool->stage_done[i], hipEventDisableTiming) != hipSuccess) {
+        pool->free_stage();
+        return GKV_ERR_HIP;
+      }
+    pool->stage_cap = cap;
+  }
+  const int k = pool->stage_i;
+  // the staging buffer's previous copy (two syncs ago) has long completed
+  // in practice; the wait only guards the case where it has not
+  if (hipEventSynchronize(pool->stage_done[k]) != hipSuccess)
     return GKV_ERR_HIP;
-  if (pool->d_ring_table &&
-      hipMemcpyAsync(pool->d_ring_table, pool->h_ring_table.data(),
-                     pool->h_ring_table.size() * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+  std::memcpy(pool->h_stage[k], pend.data(), n * sizeof(int2));
+  if (hipMemcpyAsync(pool->d_stage[k], pool->h_stage[k], n * sizeof(int2), hipMemcpyHostToDevice,
+                     s) != hipSuccess)
     return GKV_ERR_HIP;
-  // The host vectors may change right after this call returns.
-  if (hipStreamSynchronize(s) != hipSuccess)
+  hipLaunchKernelGGL(pool_scatter_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                     pool->d_table, pool->d_stage[k], (int)n);
+  if (hipGetLastError() != hipSuccess || hipEventRecord(pool->stage_done[k], s) != hipSuccess)
     return GKV_ERR_HIP;
+  pool->stage_i ^= 1;
+  pend.clear();
   return GKV_OK;
 }
 

@@ -136,8 +136,15 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
   if (HIST && (start < 0 || (start & (kBlockTokens - 1)) != 0)) {
     if (threadIdx.x == 0 && a.dev_err)
       atomicOr(a.dev_err, GKV_DEVERR_ALIGN);
-    start = 0; // the rows then attend to themselves only
+    start = 0; // (the prompt's outputs are then meaningless, but finite)
   }
+  // A full layer's cache holds positions below table_stride * 16, and the
+  // RoPE table rows the caller passes cover them: a prompt that runs past
+  // that is flagged, and its rows take their angles at the last position
+  // that fits (meaningless outputs, no read past the table).
+  const int p_cap = HIST && a.ring == 0 ? a.table_stride * kBlockTokens : INT_MAX;
+  if (HIST && start + L > p_cap && q0 == 0 && threadIdx.x == 0 && a.dev_err)
+    atomicOr(a.dev_err, GKV_DEVERR_LENGTH);
   // positions from here on: queries p0 .. p_last, keys k_lo .. p_last
   const int p0 = start + q0, p_last = start + min(q0 + kQBlock, L) - 1;
   const int W = a.window;
@@ -387,7 +394,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 8
       for (int k = wave; k < 8; k += NW) {
         const int i = 8 * (k & 3) + (lane >> 3); // the position's row in the block
         const float *tab = k < 4 ? a.cos_tab : a.sin_tab;
-        dma16(tab + (int64_t)(start + min(q0 + i, L - 1)) * (D / 2) + 4 * (lane & 7),
+        dma16(tab + (int64_t)min(start + min(q0 + i, L - 1), p_cap - 1) * (D / 2) + 4 * (lane & 7),
               ang + k * 256);
       }
     }

@@ -64,6 +64,43 @@ def test_block_accounting_and_tables(gkv, cuda):
         pool.close()
 
 
+def test_incremental_sync_tracks_the_host_tables(gkv, cuda):
+    """gkv_pool_sync sends only the changed entries, asynchronously: after
+    rounds of random reserves and frees (a free and a new reserve of the same
+    entries within one sync among them, and more changes than the staging
+    buffer first holds), the device table equals the host bookkeeping."""
+    import torch
+    rng = np.random.default_rng(7)
+    S, L = 64, 2000
+    per = (L + 15) // 16
+    pool = gkv.Pool(n_layers=1, n_kv_heads=8, max_seqs=S, max_seq_len=L, window=0,
+                    num_blocks=S * per, shuffle_seed=9)
+    try:
+        live = set()
+        stream = torch.cuda.Stream()
+        for rnd in range(12):
+            for _ in range(40):
+                if live and rng.random() < 0.3:
+                    s = int(rng.choice(sorted(live)))
+                    assert pool.free(s) == 0
+                    live.discard(s)
+                elif len(live) < S:
+                    s = pool.seq_alloc()
+                    live.add(s)
+                    assert pool.reserve(s, int(rng.integers(1, L + 1))) == 0
+            for s in list(live)[:5]:  # grow some
+                assert pool.reserve(s, L) == 0
+            pool.sync(stream)
+            stream.synchronize()
+            t = dev_table(torch, gkv, pool.view(0), S)
+            for s in range(S):
+                want = list(pool.seq_blocks(s)) if s in live else []
+                assert list(t[s, :len(want)]) == want, f"round {rnd} seq {s}"
+                assert (t[s, len(want):] == -1).all(), f"round {rnd} seq {s}"
+    finally:
+        pool.close()
+
+
 def test_sequence_ids_and_errors(gkv, cuda):
     pool = gkv.Pool(n_layers=1, n_kv_heads=8, max_seqs=2, max_seq_len=64, window=0,
                     num_blocks=8)

@@ -246,6 +246,54 @@ def test_start_not_a_block_multiple_is_flagged(oracle, gkv, cuda):
         c.pool.close()
 
 
+def test_start_not_a_block_multiple_is_flagged_cache_only(oracle, gkv, cuda):
+    """The same with every key from the cache (k = v = NULL, both chunks
+    appended first): the misaligned prompt's outputs are meaningless but
+    finite, and the error bit is set."""
+    import torch
+    c = Chunked(torch, gkv, oracle, [100, 80], [32, 48], seed=14)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    try:
+        c.append(1, err)
+        c.append(2, err)
+        got, _ = c.prefill(2, err, start=np.array([32, 40], np.int32))
+        assert int(err.item()) & gkv.DEVERR_ALIGN
+        assert np.isfinite(got).all()
+    finally:
+        c.pool.close()
+
+
+@pytest.mark.parametrize("cache_only", [False, True])
+def test_history_block_outside_the_pool_is_flagged(oracle, gkv, cuda, cache_only):
+    """A history block id outside the pool (one table entry overwritten after
+    the first chunk went in): the history prefill flags GKV_DEVERR_BLOCK_ID
+    and reads block 0 instead of faulting; every output stays finite, and the
+    prompts whose tables are intact still match the oracle."""
+    import torch
+    c = Chunked(torch, gkv, oracle, [160, 96, 130], [96, 64, 80], seed=15)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    try:
+        c.append(1, err)
+        if cache_only:
+            c.append(2, err)
+        torch.cuda.synchronize()
+        assert int(err.item()) == 0
+        # prompt 0's second history block -> an id past the pool
+        bad = torch.tensor([c.view.num_blocks + 5], dtype=torch.int32, device="cuda")
+        gkv.hip_memcpy_d2d(c.view.block_table + 4 * 1, bad.data_ptr(), 4)
+        torch.cuda.synchronize()
+        kp, vp = (None, None) if cache_only else c.packed(2)
+        got, rows = c.prefill(2, err, k=kp, v=vp)
+        assert int(err.item()) & gkv.DEVERR_BLOCK_ID
+        assert np.isfinite(got).all()
+        # prompts 1 and 2 did not use the bad entry
+        _, cu = c.chunk_rows(2)
+        keep = np.arange(cu[1], cu[3])
+        c.check(got[keep], rows[keep], "intact prompts")
+    finally:
+        c.pool.close()
+
+
 def test_v_beyond_range_is_flagged(oracle, gkv, cuda):
     """|v| >= 2^26 leaves the fp16 range of the staged v * 2^-10: the error
     word says so (the output holds inf there)."""

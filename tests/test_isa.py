@@ -70,3 +70,39 @@ def test_prefill_and_append_kernels_do_not_spill(tmp_path):
         asm = device_asm(tmp_path, src)
         for n, _, meta in kernels(asm, prefix):
             no_spills(meta, n)
+
+
+@pytest.mark.timeout(600)
+def test_direct_to_lds_scalar_bases_are_not_sign_extended(tmp_path):
+    """The history prefill's direct-to-LDS loads take a wave-uniform 64-bit base
+    in an SGPR pair (dma16_s). Its two halves are read from lane 0 with
+    v_readfirstlane, whose result the compiler types as a signed int: widened
+    as signed, a low half >= 2^31 would fill the high half with ones (a GPU
+    memory fault, seen once when the allocator happened to hand out such an
+    address). The high register of every such pair must be written by a
+    readfirstlane (or a move), never by a sign extension of the low half."""
+    asm = device_asm(tmp_path, "prefill_attention")
+    n_loads = 0
+    for n, body, _ in kernels(asm, r"prefill_kernel"):
+        lines = body.splitlines()
+        for k, l in enumerate(lines):
+            m = re.search(r"global_load_lds_dwordx4 v\d+, s\[(\d+):(\d+)\]", l)
+            if not m:
+                continue
+            n_loads += 1
+            hi = "s" + m.group(2)
+            # the last instruction before the load that writes the high register
+            for d in reversed(lines[max(0, k - 200):k]):
+                d = d.strip()
+                if re.match(r"(s_|v_)\w+ " + hi + r"\b", d) or re.match(
+                        r"(s_|v_)\w+ s\[(\d+):(\d+)\]", d) and hi in _pair_regs(d):
+                    assert re.match(r"(v_readfirstlane_b32|s_mov_b32|s_mov_b64) ", d), \
+                        f"{n}: high half {hi} of a direct-to-LDS base written by: {d}"
+                    break
+            assert not re.search(r"s_bfe_i64|s_ashr_i64", body), n
+    assert n_loads > 0
+
+
+def _pair_regs(line):
+    m = re.match(r"(s_|v_)\w+ s\[(\d+):(\d+)\]", line.strip())
+    return {"s" + str(i) for i in range(int(m.group(2)), int(m.group(3)) + 1)}
