@@ -1520,7 +1520,7 @@ __global__ __launch_bounds__(512) void decode_combine_kernel(DecodeArgs a) {
 
 // ---- host side --------------------------------------------------------------------
 
-constexpr int kRing = 4;
+constexpr int kRing = 3;
 
 // Ring depth of the split kernels (default kRing; the tuning variable
 // GKV_DECODE_RING = 3..5 picks another, read once).
@@ -1978,7 +1978,7 @@ extern "C" int gkv_yardstick_decode_loads(GKV_LAYER_PARAMS) {
   GKV_LAYER_SETUP
   AppendArgs aa = ap;
   aa.seq_lens = nullptr;
-  hipLaunchKernelGGL((decode_fused_kernel<4, 0, true>), dim3(a.n_wg),
+  hipLaunchKernelGGL((decode_fused_kernel<kRing, 0, true>), dim3(a.n_wg),
                      dim3(split_block(a.n_kv_heads)), 0, (hipStream_t)stream, a, aa, 1);
   return launch_status("decode_fused_kernel (loads only)");
 }
