@@ -405,6 +405,54 @@ int gkv_prefill_paged(void *stream, int32_t B, const int32_t *cu_seqlens,
                       const float *sinks, int32_t window, void *out, int64_t out_stride,
                       int32_t out_dtype, uint32_t *dev_err);
 
+/* ---- Exact path (fp32 caches, bit for bit with the CPU forward) ---------- */
+
+/* The reference's GPTOSS_EXACT engine build (getp-csrc/engine/gpu_engine.hpp:
+ * 478-488) keeps fp32 caches of layout [B][slots][kv_dim] (a window layer's
+ * cache a ring of `window` slots: position t in slot t % window) and runs
+ * rope_exact, kv_write_kernel and attention_exact, whose outputs equal the
+ * CPU forward's (run.cpp) bit for bit. These three entry points are that
+ * path: each result equals the reference CPU code's on the same inputs, bit
+ * for bit (the softmax's exp is glibc's expf, as the x86-64 C library with
+ * FMA computes it). Positions come either as one `pos` / `slot` for every
+ * row, as the reference engine passes them, or per row (`positions`, device
+ * int32 [B], the new token's position = length - 1). */
+
+/* rope_exact (getp-csrc/kernels/misc.hpp:55-72; run.cpp:506-526): rotates
+ * heads 0..n_heads-1 of each row in place (the query heads followed by the
+ * key heads), x1*c - x2*s and x2*c + x1*s with the first product fused.
+ * Row b takes cos/sin row positions[b] of the tables; positions NULL: row 0
+ * for every row (pass the tables' row at pos, as the reference does). */
+int gkv_rope_exact(void *stream, int32_t B, float *qkv, int64_t row_stride,
+                   const float *cos_tab, const float *sin_tab, const int32_t *positions,
+                   int32_t n_heads);
+
+/* kv_write_kernel (getp-csrc/kernels/misc.hpp:74-85): copies each row's K
+ * (kv_dim floats at row + k_off) and V (at row + v_off) into kc / vc at the
+ * row's slot: `slot` for every row, or, with positions, positions[b] (full
+ * layer, window = 0) or positions[b] % window. A slot outside [0, slots)
+ * skips the row and sets GKV_DEVERR_LENGTH in dev_err (NULL: not reported). */
+int gkv_kv_write_exact(void *stream, int32_t B, const float *qkv, int64_t row_stride,
+                       int32_t k_off, int32_t v_off, float *kc, float *vc, int32_t slots,
+                       int32_t kv_dim, int32_t slot, const int32_t *positions, int32_t window,
+                       uint32_t *dev_err);
+
+/* attention_exact (getp-csrc/kernels/attention.hpp:18-83; run.cpp:597-641):
+ * row b's query heads (q, fp32 [B][q_stride], head h at h * 64) attend to
+ * positions t0 .. p of their kv head (p = pos, or positions[b]; t0 = 0, or
+ * max(0, p - window + 1) on a window layer) plus the head's sink; out fp32
+ * [B][out_stride]. max_pos: host bound of positions[] (ignored without
+ * them). A row whose position the cache cannot hold (p >= slots on a full
+ * layer, p < 0, p > max_pos) gets zeros and GKV_DEVERR_LENGTH. A head's
+ * scores stay in LDS: GKV_ERR_CAPACITY when even one head's do not fit in
+ * what the device gives a workgroup (under 4 bytes per position of it).
+ * n_q_heads / n_kv_heads <= 16 (GKV_ERR_UNSUPPORTED otherwise). */
+int gkv_attention_exact(void *stream, int32_t B, int32_t n_q_heads, int32_t n_kv_heads,
+                        const float *q, int64_t q_stride, const float *kc, const float *vc,
+                        int32_t slots, const float *sinks, int32_t pos,
+                        const int32_t *positions, int32_t max_pos, int32_t window, float *out,
+                        int64_t out_stride, uint32_t *dev_err);
+
 /* ---- Paged KV pool (host bookkeeping, device storage) -------------------- */
 
 typedef struct gkv_pool gkv_pool;

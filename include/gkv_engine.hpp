@@ -145,17 +145,42 @@ inline void attention_q8v_chunk64(stream_t s, const float *qkv, int row_stride,
         "attention_q8v_chunk64");
 }
 
-// The reference's exact path (attention_exact, getp-csrc/kernels/attention.hpp:18-83,
-// bit-for-bit with the CPU forward) attends over fp32 caches with fp64 score
-// sums. The paged pool stores bf16 K and bf16 or int8 V, so no call here can
-// reproduce those bits: this entry point reports GKV_ERR_UNSUPPORTED (print
-// and exit, like every shim failure) instead of silently running the
-// tolerance path under the exact path's name.
-inline void attention_exact(stream_t, const float *, int, const PagedLayer &, int, float *, int,
-                            int, const PagedBatch &, bool = false) {
-  check(GKV_ERR_UNSUPPORTED, "attention_exact (fp32 caches are not built; use "
-                             "attention_bf16_chunk64 or attention_q8v_chunk64, tolerance "
-                             "2e-3 abs + 1e-2 rel)");
+// The exact path of a GPTOSS_EXACT build (gpu_engine.hpp:478-488), under the
+// reference's names and argument order (the launch configuration replaced by
+// the stream and B): fp32 caches of layout [B][slots][kv_dim] as the
+// reference keeps them (not the paged pool), one position for the batch.
+// The results equal the reference CPU forward's bit for bit.
+
+// rope_exact (getp-csrc/kernels/misc.hpp:55-72): cosv/sinv are the tables'
+// row at pos; rotates heads 0..n_heads-1 of each row in place.
+inline void rope_exact(stream_t s, int B, float *qkv, int row_stride, const float *cosv,
+                       const float *sinv, int n_heads, int head_dim) {
+  if (head_dim != 64)
+    check(GKV_ERR_UNSUPPORTED, "rope_exact (head_dim 64 only)");
+  check(gkv_rope_exact(s, B, qkv, row_stride, cosv, sinv, nullptr, n_heads), "rope_exact");
+}
+
+// kv_write_kernel (getp-csrc/kernels/misc.hpp:74-85): each row's K and V into
+// the layer's fp32 caches at `slot` (pos, or pos % window on a window layer).
+inline void kv_write_kernel(stream_t s, int B, const float *qkv, int row_stride, int k_off,
+                            int v_off, float *kc, float *vc, int slots, int slot, int kv_dim) {
+  check(gkv_kv_write_exact(s, B, qkv, row_stride, k_off, v_off, kc, vc, slots, kv_dim, slot,
+                           nullptr, 0, nullptr),
+        "kv_write_kernel");
+}
+
+// attention_exact (getp-csrc/kernels/attention.hpp:18-83): every row at
+// position pos; window 0 (full layer) or the ring of a window layer.
+inline void attention_exact(stream_t s, int B, const float *qkv, int row_stride, const float *kc,
+                            const float *vc, int slots, int kv_dim, int kv_mul,
+                            const float *sinks, float *out, int out_stride, int pos,
+                            int window) {
+  if (kv_dim % 64)
+    check(GKV_ERR_UNSUPPORTED, "attention_exact (head_dim 64 only)");
+  const int n_kv_heads = kv_dim / 64;
+  check(gkv_attention_exact(s, B, n_kv_heads * kv_mul, n_kv_heads, qkv, row_stride, kc, vc,
+                            slots, sinks, pos, nullptr, 0, window, out, out_stride, nullptr),
+        "attention_exact");
 }
 
 } // namespace gkv_engine

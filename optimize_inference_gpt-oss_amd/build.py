@@ -20,6 +20,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libgkv.so")
 DEMO = os.path.join(ROOT, "tests", "gkv_engine_demo")  # test driver of the C++ shim
+EXPF_CHECK = os.path.join(ROOT, "tests", "gkv_expf_check")  # test driver of the exact expf
 
 SOURCES = [
     "kv_append.hip",
@@ -27,6 +28,7 @@ SOURCES = [
     "prefill_attention.hip",
     "qkv_append.hip",
     "yardstick.hip",
+    "exact_attention.hip",
     "rope_table.cpp",
     "kv_pool.cpp",
     "capi.cpp",
@@ -71,8 +73,17 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"engine demo build failed:\n{r.stderr}")
     os.replace(DEMO + ".tmp", DEMO)
+    # the exhaustive check of the exact path's expf against the host C library
+    # (tests/expf_check.cpp): host code only, the header the kernels include
+    cmd = [HIPCC, "-std=c++17", "-O2", "-x", "c++", "-D__HIP_PLATFORM_AMD__", "-I", "/opt/rocm/include",
+           "-I", CSRC, "-I", os.path.join(ROOT, "include"), os.path.join(ROOT, "tests", "expf_check.cpp"),
+           "-o", EXPF_CHECK + ".tmp", "-pthread"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"expf check build failed:\n{r.stderr}")
+    os.replace(EXPF_CHECK + ".tmp", EXPF_CHECK)
     if verbose:
-        print(f"built {LIB} and {DEMO}")
+        print(f"built {LIB}, {DEMO} and {EXPF_CHECK}")
     return LIB
 
 

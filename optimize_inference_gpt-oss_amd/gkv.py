@@ -129,6 +129,11 @@ SIGNATURES = {
                                              _vp, _vp, _vp, _vp, _i32, _vp, _i64, _i32]),
     "gkv_prefill_paged": (ctypes.c_int, [_vp, _i32, _vp, _vp, _i32, _i32, _vp, _i64, _vp, _vp,
                                          _vp, _vp, CacheView, _vp, _i32, _vp, _i64, _i32, _vp]),
+    "gkv_rope_exact": (ctypes.c_int, [_vp, _i32, _vp, _i64, _vp, _vp, _vp, _i32]),
+    "gkv_kv_write_exact": (ctypes.c_int, [_vp, _i32, _vp, _i64, _i32, _i32, _vp, _vp, _i32, _i32,
+                                          _i32, _vp, _i32, _vp]),
+    "gkv_attention_exact": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, _i64, _vp, _vp, _i32, _vp,
+                                           _i32, _vp, _i32, _i32, _vp, _i64, _vp]),
     "gkv_pool_create": (ctypes.c_int, [ctypes.POINTER(PoolConfig), ctypes.POINTER(_vp)]),
     "gkv_pool_destroy": (ctypes.c_int, [_vp]),
     "gkv_pool_seq_alloc": (ctypes.c_int, [_vp, ctypes.POINTER(_i32)]),
@@ -283,6 +288,34 @@ def yardstick_gather(buf, block_ids, n_workgroups, sink, stream=None):
                                     buf.numel() * buf.element_size(), ptr(block_ids),
                                     block_ids.numel(), n_workgroups, ptr(sink))
     check("gkv_yardstick_gather", st)
+
+
+def rope_exact(qkv, cos_tab, sin_tab, n_heads, positions=None, stream=None):
+    """gkv_rope_exact: rotate heads 0..n_heads-1 of each fp32 row of qkv in place
+    (run.cpp's rounding); row b at table row positions[b] (None: row 0)."""
+    st = lib().gkv_rope_exact(stream_handle(stream), qkv.shape[0], ptr(qkv), qkv.stride(0),
+                              ptr(cos_tab), ptr(sin_tab), ptr(positions), n_heads)
+    check("gkv_rope_exact", st)
+
+
+def kv_write_exact(qkv, k_off, v_off, kc, vc, kv_dim, slot=0, positions=None, window=0,
+                   dev_err=None, stream=None):
+    """gkv_kv_write_exact: each row's K and V into fp32 caches [B][slots][kv_dim]."""
+    st = lib().gkv_kv_write_exact(stream_handle(stream), qkv.shape[0], ptr(qkv), qkv.stride(0),
+                                  k_off, v_off, ptr(kc), ptr(vc), kc.shape[1], kv_dim, slot,
+                                  ptr(positions), window, ptr(dev_err))
+    check("gkv_kv_write_exact", st)
+
+
+def attention_exact(q, n_q_heads, n_kv_heads, kc, vc, sinks, out, pos=0, positions=None,
+                    max_pos=0, window=0, dev_err=None, stream=None):
+    """gkv_attention_exact: decode attention over fp32 caches [B][slots][kv_dim],
+    bit for bit with run.cpp's CPU forward."""
+    st = lib().gkv_attention_exact(stream_handle(stream), q.shape[0], n_q_heads, n_kv_heads,
+                                   ptr(q), q.stride(0), ptr(kc), ptr(vc), kc.shape[1],
+                                   ptr(sinks), pos, ptr(positions), max_pos, window, ptr(out),
+                                   out.stride(0), ptr(dev_err))
+    check("gkv_attention_exact", st)
 
 
 def workspace_bytes(B, n_kv_heads, max_seq_len, window=0, split_tokens=0) -> int:

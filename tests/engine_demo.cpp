@@ -44,13 +44,17 @@
 
 int main(int argc, char **argv) {
   if (argc != 3 && argc != 4) {
-    fprintf(stderr, "usage: %s in.bin out.bin [fused | project | q8v]\n", argv[0]);
+    fprintf(stderr, "usage: %s in.bin out.bin [fused | project | q8v | planned | exact]\n",
+            argv[0]);
     return 2;
   }
   const bool fused = argc == 4 && std::string(argv[3]) == "fused";
   const bool project = argc == 4 && std::string(argv[3]) == "project";
   const bool q8v = argc == 4 && std::string(argv[3]) == "q8v";
   const bool planned = argc == 4 && std::string(argv[3]) == "planned";
+  // exact: the GPTOSS_EXACT trio over fp32 caches [B][slots][kv_dim] per layer
+  // (window layers: a ring of W slots), fp32 outputs
+  const bool exact = argc == 4 && std::string(argv[3]) == "exact";
   FILE *f = fopen(argv[1], "rb");
   if (!f)
     return 2;
@@ -140,6 +144,18 @@ int main(int argc, char **argv) {
   }
   gkv_engine::PagedBatch bt{d_pos, d_lens, P, d_cos, d_sin, d_ws, ws_bytes, d_err};
 
+  std::vector<float *> kc32(NL, nullptr), vc32(NL, nullptr);
+  std::vector<int> slots32(NL, 0);
+  float *d_out32 = nullptr;
+  if (exact) {
+    for (int l = 0; l < NL; l++) {
+      slots32[l] = layers[l].window > 0 ? layers[l].window : P;
+      HIP_OK(hipMalloc(&kc32[l], (size_t)B * slots32[l] * Hkv * 64 * 4));
+      HIP_OK(hipMalloc(&vc32[l], (size_t)B * slots32[l] * Hkv * 64 * 4));
+    }
+    HIP_OK(hipMalloc(&d_out32, (size_t)B * ATT * 4));
+  }
+  std::vector<float> out32(exact ? (size_t)P * NL * B * ATT : 0);
   std::vector<uint16_t> out((size_t)P * NL * B * ATT);
   std::vector<int32_t> pos(B), lens(B);
   for (int p = 0; p < P; p++) {
@@ -161,7 +177,21 @@ int main(int argc, char **argv) {
       } else {
         HIP_OK(hipMemcpyAsync(d_qkv, qkv.data() + ((size_t)p * NL + l) * B * QKV,
                               (size_t)B * QKV * 4, hipMemcpyHostToDevice, s));
-        if (fused) {
+        if (exact) {
+          // layer_attention's exact lines (gpu_engine.hpp:480-486)
+          const int KVD = Hkv * 64, slot = layers[l].window > 0 ? p % layers[l].window : p;
+          gkv_engine::rope_exact(s, B, d_qkv, QKV, d_cos + (size_t)p * 32, d_sin + (size_t)p * 32,
+                                 Hq + Hkv, 64);
+          gkv_engine::kv_write_kernel(s, B, d_qkv, QKV, ATT, ATT + KVD, kc32[l], vc32[l],
+                                      slots32[l], slot, KVD);
+          gkv_engine::attention_exact(s, B, d_qkv, QKV, kc32[l], vc32[l], slots32[l], KVD,
+                                      Hq / Hkv, layers[l].sinks, d_out32, ATT, p,
+                                      layers[l].window);
+          HIP_OK(hipMemcpyAsync(out32.data() + ((size_t)p * NL + l) * B * ATT, d_out32,
+                                (size_t)B * ATT * 4, hipMemcpyDeviceToHost, s));
+          HIP_OK(hipStreamSynchronize(s));
+          continue;
+        } else if (fused) {
           gkv_engine::rope_kv_attention_bf16(s, B, d_qkv, QKV, layers[l], Hq, d_out, ATT, bt);
         } else if (planned) {
           const bool window_kind = layers[l].window > 0;
@@ -191,7 +221,10 @@ int main(int argc, char **argv) {
     return 1;
   }
   FILE *g = fopen(argv[2], "wb");
-  if (!g || fwrite(out.data(), 2, out.size(), g) != out.size())
+  if (!g)
+    return 2;
+  if (exact ? fwrite(out32.data(), 4, out32.size(), g) != out32.size()
+            : fwrite(out.data(), 2, out.size(), g) != out.size())
     return 2;
   fclose(g);
   gkv_pool_destroy(pool);
@@ -200,6 +233,11 @@ int main(int argc, char **argv) {
                     (void *)d_w,
                     (void *)d_b})
     (void)hipFree(ptr);
+  for (int l = 0; l < NL; l++) {
+    (void)hipFree(kc32[l]);
+    (void)hipFree(vc32[l]);
+  }
+  (void)hipFree(d_out32);
   (void)hipStreamDestroy(s);
   printf("engine demo: %d steps x %d layers x %d sequences ok\n", P, NL, B);
   return 0;

@@ -106,3 +106,41 @@ def test_engine_shim_rejects_mismatched_cache(cuda, tmp_path, mode, v_int8):
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=90)
     assert r.returncode != 0
     assert "attention_" in r.stderr and "bad argument" in r.stderr, r.stderr
+
+
+def test_engine_shim_exact_loop(oracle, cuda, tmp_path):
+    """The GPTOSS_EXACT trio through the shim (rope_exact, kv_write_kernel,
+    attention_exact in layer_attention's order, fp32 caches per layer, a
+    32-slot ring on the window layer): every step's fp32 output equals the
+    CPU oracle's bit for bit."""
+    if not os.path.exists(DEMO):
+        pytest.fail("gkv_engine_demo is not built (run __graft_entry__.build())")
+    P, B, Hq, Hkv, NL, W = 40, 3, 64, 8, 2, 32
+    rng = np.random.default_rng(2025)
+    QKV = (Hq + 2 * Hkv) * 64
+    qkv = (rng.standard_normal((P, NL, B, QKV)) * 0.5).astype(np.float32)
+    sinks = rng.standard_normal((NL, Hq)).astype(np.float32)
+    inp, outp = tmp_path / "in.bin", tmp_path / "out.bin"
+    with open(inp, "wb") as f:
+        np.array([P, B, Hq, Hkv, NL, W, 0], np.int32).tofile(f)
+        qkv.tofile(f)
+        sinks.tofile(f)
+    r = subprocess.run([DEMO, str(inp), str(outp), "exact"], capture_output=True, text=True,
+                       timeout=90)
+    assert r.returncode == 0, r.stderr
+    got = np.fromfile(outp, np.float32).reshape(P, NL, B, Hq, 64)
+    cos, sin = oracle.rope_table(P)
+    for l in range(NL):
+        window = W if l % 2 == 0 else 0
+        kc = np.zeros((B, P, Hkv, 64), np.float32)
+        vc = np.zeros((B, P, Hkv, 64), np.float32)
+        for p in range(P):
+            pos = np.full(B, p, np.int32)
+            q_rot, k_rot, _, _ = oracle.kv_append(qkv[p, l], Hq, Hkv, cos, sin, pos)
+            kc[:, p] = k_rot
+            vc[:, p] = qkv[p, l][:, (Hq + Hkv) * 64:].reshape(B, Hkv, 64)
+            ref = oracle.decode_attention(q_rot, kc[:, :p + 1], vc[:, :p + 1], pos, sinks[l],
+                                          window=window)
+            g = np.ascontiguousarray(got[p, l]).view(np.uint32)
+            w = np.ascontiguousarray(ref).view(np.uint32)
+            assert (g == w).all(), f"layer {l} step {p}: {(g != w).sum()} values differ"
