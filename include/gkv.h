@@ -167,7 +167,9 @@ int gkv_kv_append(void *stream, int32_t n_rows, const float *qkv, int64_t row_st
  *   x      bf16 [rows][x_stride], x_stride a multiple of 8, 16-byte aligned
  *   w_qkv  bf16 [(Hq + 2 Hkv) * 64][hidden] row-major, 16-byte aligned
  *   b_qkv  fp32 [(Hq + 2 Hkv) * 64] or NULL
- * hidden is a multiple of 64 (GKV_ERR_UNSUPPORTED otherwise). */
+ * hidden is a multiple of 64 (GKV_ERR_UNSUPPORTED otherwise). For decode
+ * steps (hundreds of rows); at prompt sizes (thousands of rows) a library
+ * GEMM followed by gkv_kv_append is faster. */
 int gkv_qkv_append(void *stream, int32_t n_rows, const void *x, int64_t x_stride,
                    int32_t hidden, const void *w_qkv, const float *b_qkv, int32_t n_q_heads,
                    const float *cos_tab, const float *sin_tab, const int32_t *row_pos,

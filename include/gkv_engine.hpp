@@ -69,7 +69,9 @@ inline void rope_kv_bf16(stream_t s, int B, float *qkv, int row_stride, const Pa
 // C = A . W^T + bias into fp32 rows (the Q part left unrotated, as gemm_bf16
 // writes it) and each row's rotated K and its V stored into the layer's paged
 // cache at its position, in one gkv_qkv_append call. N must be
-// (n_q_heads + 2 Hkv) * 64.
+// (n_q_heads + 2 Hkv) * 64. Meant for decode steps (hundreds of rows, where
+// it runs level with the pair); for prompt-sized batches (thousands of rows)
+// keep the library GEMM followed by rope_kv_bf16, which is faster there.
 inline void gemm_bf16_rope_kv(stream_t s, const bf16_t *A, int M, const bf16_t *W,
                               const float *bias, float *C, int N, int K, const PagedBatch &bt,
                               int n_q_heads, const PagedLayer &layer) {
