@@ -337,6 +337,9 @@ def run_prefill(torch, gkv, args) -> int:
             k=torch.empty(T, Hkv * D, dtype=torch.bfloat16, device=dev),
             v=torch.empty(T, Hkv * D, dtype=torch.bfloat16, device=dev),
             out=torch.empty(T, Hq * D, dtype=torch.bfloat16, device=dev)))
+    # --prefill-layer: one kind only (a profile of one layer kind's launches)
+    if args.prefill_layer != "both":
+        layers = [ly for ly in layers if (ly["window"] == 0) == (args.prefill_layer == "full")]
     stream = torch.cuda.current_stream()
 
     def flops(window):
@@ -395,7 +398,7 @@ def run_prefill(torch, gkv, args) -> int:
     for li, e in ev:
         kern.setdefault(li, []).append((e[0].elapsed_time(e[1]), e[1].elapsed_time(e[2])))
     fl = [flops(ly["window"]) for ly in layers]
-    full = [i for i, ly in enumerate(layers) if not ly["window"]][0]
+    full = ([i for i, ly in enumerate(layers) if not ly["window"]] or [0])[0]
     dom_ms = float(np.mean([x[1] for x in kern[full]]))
     tflops = fl[full] / (dom_ms * 1e-3) / 1e12
     # Algorithmic bytes of one prefill launch: the fp32 query of every row
@@ -407,6 +410,8 @@ def run_prefill(torch, gkv, args) -> int:
     traffic, traffic_note = load_traffic("prefill_config4_traffic")
     if args.prefill_from_cache or args.v_int8 or args.kv_fp8:
         traffic, traffic_note = None, "the traffic profile covers packed rows and a bf16 cache"
+    if args.prefill_layer == "window":
+        traffic, traffic_note = None, "the traffic profile covers the full layer's launch"
     line = {
         "metric": "causal prefill attention throughput (TFLOP/s), config 4",
         "value": round(sum(fl) / (ms_per_step * 1e-3) / 1e12, 2),
@@ -421,6 +426,7 @@ def run_prefill(torch, gkv, args) -> int:
             "kv_cache": "e4m3 K and V + scales" if args.kv_fp8 else
                         "bf16 K, int8+scale V" if args.v_int8 else "bf16",
             "full_layer_keys": "paged cache" if args.prefill_from_cache else "packed rows",
+            "layers": args.prefill_layer,
             "kernel_ms": {("window" if layers[i]["window"] else "full"): {
                 "append": round(float(np.mean([x[0] for x in kern[i]])), 4),
                 "prefill": round(float(np.mean([x[1] for x in kern[i]])), 4)}
@@ -623,6 +629,9 @@ def main() -> int:
     ap.add_argument("--no-plan-reuse", action="store_true",
                     help="several layers: every layer plans (gkv_decode_layer) instead of the "
                          "first of each kind keeping its plan and the others reusing it")
+    ap.add_argument("--prefill-layer", default="both", choices=["both", "full", "window"],
+                    help="config 4: run both layer kinds (default) or one (to profile one "
+                         "kind's launches; the dominant kernel is then that kind's)")
     ap.add_argument("--prefill-from-cache", action="store_true",
                     help="config 4: the full layer's append writes the paged cache only and the "
                          "prefill reads every key from it (gkv_prefill_paged) instead of from "

@@ -1304,7 +1304,7 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
   if (append && wave < n_seq) {
     const int b = b_first + wave;
     if (new_token_in_range(b)) {
-      first_row = append_begin(ap, b, lane, len_of(b) - 1);
+      first_row = append_begin(ap, b, lane, len_of(b) - 1, /*direct=*/true);
       first_b = b;
     }
   }
@@ -1376,7 +1376,7 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
     for (int j = wave + n_waves; j < n_seq; j += n_waves) {
       const int b = b_first + j;
       if (new_token_in_range(b))
-        append_row(ap, b, lane, 0, 1, nullptr, len_of(b) - 1);
+        append_row(ap, b, lane, 0, 1, nullptr, len_of(b) - 1, /*direct=*/true);
     }
   }
 

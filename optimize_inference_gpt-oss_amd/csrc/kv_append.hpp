@@ -208,13 +208,14 @@ struct RowPlace {
 // stay adjacent in one wave (the int8 scale is their max). v_stage: NULL, or
 // bf16 [Hkv * 64] in LDS that receives the row's V; then the bf16 V cache
 // store is left to the caller. pos_known >= 0: the row's position, already
-// known to the caller (no load of row_pos / seq_lens).
+// known to the caller (no load of row_pos / seq_lens). direct: as for
+// append_begin below (row r is sequence r's new token at pos_known).
 __device__ __forceinline__ RowPlace append_row(const AppendArgs &a, int r, int lane,
                                                int part = 0, int n_parts = 1,
                                                uint16_t *v_stage = nullptr,
-                                               int pos_known = -1) {
+                                               int pos_known = -1, bool direct = false) {
   constexpr int D = kHeadDim, HALF = kHeadDim / 2;
-  const int seq = a.row_seq ? a.row_seq[r] : r;
+  const int seq = direct || !a.row_seq ? r : a.row_seq[r];
   // the row's position: given, or the last position of its sequence
   const int pos = pos_known >= 0 ? pos_known : a.row_pos ? a.row_pos[r] : a.seq_lens[seq] - 1;
   const float *row = a.qkv + (int64_t)r * a.row_stride;
@@ -237,7 +238,7 @@ __device__ __forceinline__ RowPlace append_row(const AppendArgs &a, int r, int l
   // Where the token goes in the paged cache (if anywhere).
   const int slot = a.ring > 0 ? pos % a.ring : pos;
   bool store = a.kc != nullptr;
-  if (store && a.ring > 0 && a.seq_lens && pos + a.ring < a.seq_lens[seq])
+  if (!direct && store && a.ring > 0 && a.seq_lens && pos + a.ring < a.seq_lens[seq])
     store = false; // a later row of this call takes the ring slot
   int64_t kbase = 0, vbase = 0;
   const int off = slot % kBlockTokens;
@@ -289,7 +290,11 @@ __device__ __forceinline__ RowPlace append_row(const AppendArgs &a, int r, int l
 // and the angles), append_end rotates, rounds and stores, as append_row does.
 // One wave per row, at most 8 kv heads, no rotated-query output. pos: the
 // row's position if the caller knows it, else -1 (row_pos[r], or the last
-// position of its sequence).
+// position of its sequence). direct: row r is sequence r's new token at pos
+// (>= 0) and no later row of the call takes its ring slot, so neither
+// row_seq nor seq_lens is read: every load then goes out at once (a possible
+// load of either, even one not taken, makes the compiler wait for all the
+// loads before it, one round trip each).
 struct AppendLoads {
   int seq, slot, off, table_entry; // table_entry: the block id as loaded (-1: none)
   bool store;
@@ -298,7 +303,7 @@ struct AppendLoads {
 };
 
 __device__ __forceinline__ AppendLoads append_begin(const AppendArgs &a, int r, int lane,
-                                                    int pos) {
+                                                    int pos, bool direct = false) {
   constexpr int D = kHeadDim, HALF = kHeadDim / 2;
   AppendLoads L;
   // The same four loads on every lane (no divergent branch, so the loaded
@@ -315,13 +320,13 @@ __device__ __forceinline__ AppendLoads append_begin(const AppendArgs &a, int r, 
   L.x[1] = *(const f32x4 *)(xp + 4);
   L.x[2] = *(const f32x4 *)(xp + second);
   L.x[3] = *(const f32x4 *)(xp + second + 4);
-  L.seq = a.row_seq ? a.row_seq[r] : r;
-  if (pos < 0)
+  L.seq = direct || !a.row_seq ? r : a.row_seq[r];
+  if (!direct && pos < 0)
     pos = a.row_pos ? a.row_pos[r] : a.seq_lens[L.seq] - 1;
   L.slot = a.ring > 0 ? pos % a.ring : pos;
   L.off = L.slot % kBlockTokens;
   L.store = a.kc != nullptr;
-  if (L.store && a.ring > 0 && a.seq_lens && pos + a.ring < a.seq_lens[L.seq])
+  if (!direct && L.store && a.ring > 0 && a.seq_lens && pos + a.ring < a.seq_lens[L.seq])
     L.store = false; // a later row of this call takes the ring slot
   const int blk = L.slot / kBlockTokens;
   L.table_entry = L.store && blk < a.table_stride
