@@ -958,6 +958,7 @@ void decode_split_kernel(DecodeArgs a) {
 // ---- fused: plan, append and split in one launch --------------------------------
 
 constexpr int kStepsPerThread = kInfoSlab / 64; // record-building steps per thread (>= 64 threads)
+constexpr int kShortRun = 8; // sequences per range counted rather than searched (records)
 
 // Tokens of a sequence of length L in the stream: its length, or the window,
 // clamped to what the table row and the launch were sized for.
@@ -1060,6 +1061,7 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
   __shared__ int s_wave[kSplitWaves];
   __shared__ int s_max[kSplitWaves];
   __shared__ int s_hash[2 * kSplitWaves];
+  __shared__ int s_find[2];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nt = blockDim.x, B = a.B;
   const int n_waves = nt >> 6;
   const int w_id = blockIdx.x;
@@ -1231,28 +1233,22 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
     // last one starting before re. (The first is found for a range without
     // tokens too, when rs < T: the combine needs the sequence that every
     // range, empty or not, starts inside of.)
-    if (rs < T) {
-      int lo = 0, hi = B - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (s_cu[mid] <= rs)
-          lo = mid;
-        else
-          hi = mid - 1;
-      }
-      b_first = lo;
+    // One pass over the prefix sums, a thread per candidate (two LDS reads
+    // each, then one barrier) instead of two binary searches of dependent
+    // LDS reads: exactly one b has cu[b] <= rs < cu[b + 1] (rs < T = cu[B]),
+    // and exactly one b > b_first has cu[b - 1] < re <= cu[b] (rs < re <= T).
+    for (int b = t; b <= B; b += nt) {
+      const int c = s_cu[b];
+      if (b < B && rs < T && c <= rs && s_cu[b + 1] > rs)
+        s_find[0] = b;
+      if (b >= 1 && rs < re && c >= re && s_cu[b - 1] < re)
+        s_find[1] = b;
     }
-    if (rs < re) {
-      int lo = b_first, hi = B; // the first b with cu[b] >= re (cu[B] = T >= re)
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (s_cu[mid] >= re)
-          hi = mid;
-        else
-          lo = mid + 1;
-      }
-      n_seq = lo - b_first;
-    }
+    __syncthreads();
+    if (rs < T)
+      b_first = s_find[0];
+    if (rs < re)
+      n_seq = s_find[1] - b_first;
     if (keep && t == 0)
       kept_ranges[w_id] = int4{rs, max(re, rs), b_first, n_seq};
     if (a.aligned && t == 0)
@@ -1344,13 +1340,23 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
       rcd[k] = 0;
       if (i < n_steps) {
         const int tok = rs + i * kStep;
-        int lo = 0, hi = B - 1; // the sequence holding the step: last b with cu[b] <= tok
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) >> 1;
-          if (s_cu[mid] <= tok)
-            lo = mid;
-          else
-            hi = mid - 1;
+        // the sequence holding the step: the last b with cu[b] <= tok, one
+        // of the range's run b_first .. b_first + n_seq - 1; a short run is
+        // counted with independent LDS reads, a long one searched
+        int lo = b_first;
+        if (n_seq <= kShortRun) {
+#pragma unroll
+          for (int j = 1; j < kShortRun; j++)
+            lo += j < n_seq && s_cu[b_first + j] <= tok ? 1 : 0;
+        } else {
+          int hi = b_first + n_seq - 1;
+          while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s_cu[mid] <= tok)
+              lo = mid;
+            else
+              hi = mid - 1;
+          }
         }
         const int b = lo;
         const int off = tok - s_cu[b];
