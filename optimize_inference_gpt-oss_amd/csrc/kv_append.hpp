@@ -306,6 +306,15 @@ __device__ __forceinline__ AppendLoads append_begin(const AppendArgs &a, int r, 
                                                     int pos, bool direct = false) {
   constexpr int D = kHeadDim, HALF = kHeadDim / 2;
   AppendLoads L;
+  // The row's index loads (its sequence and position) go out first, then its
+  // K or V pieces, so the wait for the indices leaves the pieces in flight;
+  // then every load that depends on the indices (the length for the ring
+  // rule, the table entry, the angles) goes out at once. The table entry is
+  // loaded whether or not the ring rule keeps the store.
+  const int seq = direct || !a.row_seq ? r : a.row_seq[r];
+  const bool pos_from_len = !direct && pos < 0 && !a.row_pos;
+  if (!direct && pos < 0 && a.row_pos)
+    pos = a.row_pos[r];
   // The same four loads on every lane (no divergent branch, so the loaded
   // registers are not merged through memory): a key lane's dims 8j..+7 and
   // 32+8j..+7, a value lane's 16q..16q+15; lanes past the heads re-read the
@@ -320,18 +329,18 @@ __device__ __forceinline__ AppendLoads append_begin(const AppendArgs &a, int r, 
   L.x[1] = *(const f32x4 *)(xp + 4);
   L.x[2] = *(const f32x4 *)(xp + second);
   L.x[3] = *(const f32x4 *)(xp + second + 4);
-  L.seq = direct || !a.row_seq ? r : a.row_seq[r];
-  if (!direct && pos < 0)
-    pos = a.row_pos ? a.row_pos[r] : a.seq_lens[L.seq] - 1;
+  L.seq = seq;
+  if (pos_from_len)
+    pos = a.seq_lens[L.seq] - 1;
   L.slot = a.ring > 0 ? pos % a.ring : pos;
   L.off = L.slot % kBlockTokens;
+  const int blk = L.slot / kBlockTokens;
+  L.table_entry = a.kc != nullptr && blk < a.table_stride
+                      ? a.table[(int64_t)L.seq * a.table_stride + blk]
+                      : -1;
   L.store = a.kc != nullptr;
   if (!direct && L.store && a.ring > 0 && a.seq_lens && pos + a.ring < a.seq_lens[L.seq])
     L.store = false; // a later row of this call takes the ring slot
-  const int blk = L.slot / kBlockTokens;
-  L.table_entry = L.store && blk < a.table_stride
-                      ? a.table[(int64_t)L.seq * a.table_stride + blk]
-                      : -1;
   const float *cp = a.cos_tab + (int64_t)pos * HALF + 8 * j;
   const float *sp = a.sin_tab + (int64_t)pos * HALF + 8 * j;
   L.cs[0] = *(const f32x4 *)cp;
