@@ -111,6 +111,8 @@ def _attention_case(seed, B, Hq, Hkv, lens_lo, lens_hi, window=0, slots=None):
     ("config2_shape", 6, 64, 8, 128, 2048, 0),   # gpt-oss-20b shape, fewer sequences
     ("window_ring", 8, 64, 8, 1, 4096, 128),     # 128-slot rings, partial and full windows
     ("long", 2, 16, 2, 9000, 12000, 0),          # score rows past a workgroup's LDS for 8 heads
+    ("group16", 3, 32, 2, 1, 3000, 0),           # 16 query heads per kv head (1024 threads)
+    ("group1", 3, 4, 4, 1, 700, 64),             # one query head per kv head, a 64-slot ring
 ])
 def test_attention_exact_bit_exact(gkv, cuda, name, B, Hq, Hkv, lo, hi, window):
     import torch
