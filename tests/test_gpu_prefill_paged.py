@@ -18,7 +18,8 @@ every position, run.cpp:597-642) within max-abs 2e-3 + rel 1e-2.
   reference's quantize_v; e4m3: value(code) * scale of the rotated K and of
   V, orc_quantize_fp8), those from packed rows for their bf16 values.
 - Error words: a start that is not a multiple of 16, and a V beyond the
-  prefill's range.
+  prefill's range (bf16 and int8 V); small V (|v| ~ 1e-2 and 2^-20) within
+  the tolerance.
 """
 import numpy as np
 import pytest
@@ -45,11 +46,8 @@ class Chunked:
         self.sinks = rng.standard_normal(Hq).astype(np.float32)
         pos = np.concatenate([np.arange(n) for n in self.L]).astype(np.int32)
         cos, sin = oracle.rope_table(int(self.L.max()))
-        q_rot, k_rot, kb, vb = oracle.kv_append(self.qkv, Hq, Hkv, cos, sin, pos)
-        self.oracle, self.q_rot, self.k_f = oracle, q_rot, oracle.from_bf16(kb)
-        self.v_bf = oracle.from_bf16(vb)
-        self.ref = oracle.prefill_attention(cu, q_rot, self.k_f, self.v_bf, self.sinks,
-                                            window=window)
+        self.oracle, self.cu_all, self.pos, self.cos, self.sin = oracle, cu, pos, cos, sin
+        k_rot = self.reference()
         # what a quantized cache stands for: the fp32 (rotated K and) V quantized per
         # token and head
         self.fmt = fmt
@@ -60,7 +58,6 @@ class Chunked:
         elif fmt == "fp8":
             self.k_q = oracle.dequantize_fp8(*oracle.quantize_fp8(k_rot.reshape(T, Hkv, D)))
             self.v_q = oracle.dequantize_fp8(*oracle.quantize_fp8(v32))
-        self.cu_all, self.pos = cu, pos
         # the pool: one layer (a ring layer when window > 0), NaN in every slot
         self.pool = gkv.Pool(n_layers=1, n_kv_heads=Hkv, max_seqs=self.B,
                              max_seq_len=int(self.L.max()), window=window,
@@ -86,6 +83,17 @@ class Chunked:
         self.t = t
         self.cos_d, self.sin_d = t(cos), t(sin)
         self.sinks_d = t(self.sinks)
+
+    def reference(self):
+        """The oracle's prefill of the whole prompts from the current qkv rows
+        (call again after changing them); returns the rotated fp32 keys."""
+        o = self.oracle
+        q_rot, k_rot, kb, vb = o.kv_append(self.qkv, self.Hq, self.Hkv, self.cos, self.sin,
+                                           self.pos)
+        self.q_rot, self.k_f, self.v_bf = q_rot, o.from_bf16(kb), o.from_bf16(vb)
+        self.ref = o.prefill_attention(self.cu_all, q_rot, self.k_f, self.v_bf, self.sinks,
+                                       window=self.window)
+        return k_rot
 
     def chunk_rows(self, which):
         """Rows (indices into the whole-prompt arrays) of chunk 1 or 2, prompt by prompt."""
@@ -296,16 +304,40 @@ def test_history_block_outside_the_pool_is_flagged(oracle, gkv, cuda, cache_only
 
 def test_v_beyond_range_is_flagged(oracle, gkv, cuda):
     """|v| >= 2^26 leaves the fp16 range of the staged v * 2^-10: the error
-    word says so (the output holds inf there)."""
+    word says so (the output holds inf there), on the bf16 and on the int8-V
+    cache."""
     import torch
-    c = Chunked(torch, gkv, oracle, [64], [32], seed=14)
-    Hq, Hkv = c.Hq, c.Hkv
-    c.qkv[40, (Hq + Hkv) * D + 5] = 2.0 ** 27  # chunk 2, V of kv head 0, dim 5
+    for fmt in ("bf16", "int8"):
+        c = Chunked(torch, gkv, oracle, [64], [32], seed=14, fmt=fmt)
+        Hq, Hkv = c.Hq, c.Hkv
+        c.qkv[40, (Hq + Hkv) * D + 5] = 2.0 ** 27  # chunk 2, V of kv head 0, dim 5
+        err = torch.zeros(1, dtype=torch.int32, device="cuda")
+        try:
+            c.append(1, err)
+            kp, vp = c.packed(2)
+            c.prefill(2, err, k=kp, v=vp)
+            assert int(err.item()) & gkv.DEVERR_RANGE, fmt
+        finally:
+            c.pool.close()
+
+
+def test_small_v_within_tolerance(oracle, gkv, cuda):
+    """Below the staged range (|v| < 2^-4, fp16 of v * 2^-10 subnormal) the
+    error stays within 2^-15 absolute: values of 2^-20 and 3e-3 in the cached
+    history and in the chunk are attended within the tolerance, with no error
+    word."""
+    import torch
+    c = Chunked(torch, gkv, oracle, [100, 70], [48, 32], seed=15, scale=0.01)
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    Hq, Hkv = c.Hq, c.Hkv
+    v0 = (Hq + Hkv) * D
+    c.qkv[60, v0 + 9] = 2.0 ** -20
+    c.reference()
     try:
         c.append(1, err)
         kp, vp = c.packed(2)
-        c.prefill(2, err, k=kp, v=vp)
-        assert int(err.item()) & gkv.DEVERR_RANGE
+        got, rows = c.prefill(2, err, k=kp, v=vp)
+        assert int(err.item()) == 0
+        c.check(got, rows, "small V")
     finally:
         c.pool.close()
