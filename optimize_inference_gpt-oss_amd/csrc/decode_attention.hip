@@ -200,6 +200,8 @@ __device__ __forceinline__ bf16x8 pack_pieces(const float (&x)[8], bool lo) {
 }
 
 // Four int8 codes (one per byte) -> four bf16 (exact: |code| <= 127), in order.
+// (Each conversion compiles to one v_cvt_f32_i32 with a sign-extended byte
+// select.)
 __device__ __forceinline__ u32x2 int8x4_to_bf16x4(uint32_t w) {
   uint32_t h[4];
 #pragma unroll
@@ -826,8 +828,11 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
         const bool blk_bad = (bad >> jt) & 1;
 #pragma unroll
         for (int r = 0; r < 4; r++)
-          if (16 * jt + 4 * kg + r >= valid || blk_bad)
+          if (16 * jt + 4 * kg + r >= valid || blk_bad) {
             sc[4 * jt + r] = -INFINITY;
+            if (VQ) // its weight is 0; its scale (possibly never written) too
+              vr[2 + jt][r] = 0u;
+          }
         if (KF8) {
           // e4m3 codes of unwritten slots may be NaN: zero them
           uint32_t keep = 0;
@@ -879,12 +884,10 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
     }
     if (VQ) {
       // int8 / e4m3 V: the token's scale goes into its weight (the codes are
-      // exact in bf16); a masked token's weight is 0 whatever its scale holds
+      // exact in bf16); a masked token's weight and scale are both 0
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float sc_t = __uint_as_float(vr[2 + (i >> 2)][i & 3]);
-        p[i] = p[i] == 0.0f ? 0.0f : p[i] * sc_t;
-      }
+      for (int i = 0; i < 8; i++)
+        p[i] *= __uint_as_float(vr[2 + (i >> 2)][i & 3]);
       const bf16x8 pop = pack_pieces(p, lo);
 #pragma unroll
       for (int nn = 0; nn < 4; nn++) {
