@@ -89,6 +89,7 @@ constexpr int kInfoSlab = kMaxRange / kStep;      // step records per range
 constexpr int kSplitWaves = 4;         // split kernel: one wave per SIMD
 constexpr int kStageRecs = 8;          // finished segments a stream wave holds in LDS
 constexpr int kSplitThreads = 64 * kSplitWaves;
+constexpr int kMaxSplitWaves = 8;      // the fused kernel's 8-wave form: two waves per SIMD
 constexpr int kPrepThreads = 1024;
 constexpr int kMaxBatch = 8192;        // sequences per call (prefix sums kept in LDS)
 constexpr int kBadBlock = -1;          // F entry: id outside the pool
@@ -467,7 +468,7 @@ __global__ __launch_bounds__(kPrepThreads) void decode_layer_prep_kernel(DecodeA
 // LO: loads only (the ceiling yardstick): every load of the stream is issued
 // and waited for exactly as in the attention, and its data is folded into an
 // XOR instead of the softmax and the matrix ops; nothing useful is written.
-template <int R, int VF, bool RAWQ, bool LO = false>
+template <int R, int VF, bool RAWQ, bool LO = false, int NWV = kSplitWaves>
 __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, const int2 *s_ids,
                                              const int *s_rec, const int *s_len, int n_steps) {
   constexpr int D = kHeadDim;
@@ -635,9 +636,10 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
   // that hold outputs (lane (kg, col < 8): query head col, dims 4 kg + 16 nn
   // + 0..3), the (m, l) of each query head for a partial, and what the record
   // is (a whole sequence's output, scaled, or a partial for the combine).
-  __shared__ f32x4 s_st_o[kSplitWaves][kStageRecs][32][4];
-  __shared__ float2 s_st_ml[kSplitWaves][kStageRecs][kCols];
-  __shared__ int4 s_st_meta[kSplitWaves][kStageRecs];
+  constexpr int kRecs = kStageRecs * kSplitWaves / NWV; // the same LDS for 4 or 8 waves
+  __shared__ f32x4 s_st_o[NWV][kRecs][32][4];
+  __shared__ float2 s_st_ml[NWV][kRecs][kCols];
+  __shared__ int4 s_st_meta[NWV][kRecs];
   int n_staged = 0; // wave-uniform
   const bool out_lane = !lo && head_ok;
   const int st_lane = kg * 8 + head;
@@ -695,7 +697,7 @@ __device__ __forceinline__ void stream_range(const DecodeArgs &a, int w_id, cons
         oo[nn][r] = o[nn][r] + swap8(o[nn][r]);
     if (cur_key < 0)
       return;
-    if (n_staged == kStageRecs) // full (many short sequences): to memory now
+    if (n_staged == kRecs) // full (many short sequences): to memory now
       write_out();
     const bool whole = cur_whole && cur_ends;
     if (out_lane) {
@@ -1054,16 +1056,16 @@ __device__ __forceinline__ int plan_key(const DecodeArgs &a, int i, uint2 lh) {
 // one kind in one decode step share the lengths and the table, so one keeps
 // and the others reuse; the ranges, and so every output bit, are the same
 // either way.
-template <int R, int VF, bool LO = false>
-__global__ __launch_bounds__(kSplitThreads) __attribute__((amdgpu_waves_per_eu(1)))
+template <int R, int VF, bool LO = false, int NWV = kSplitWaves>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(NWV / kSplitWaves)))
 void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
   __shared__ int s_cu[kMaxBatch + 1];
   __shared__ int s_len[kMaxBatch];
   __shared__ int2 s_ids[kIdSlab / 2];
   __shared__ int s_rec[kInfoSlab];
-  __shared__ int s_wave[kSplitWaves];
-  __shared__ int s_max[kSplitWaves];
-  __shared__ int s_hash[2 * kSplitWaves];
+  __shared__ int s_wave[kMaxSplitWaves];
+  __shared__ int s_max[kMaxSplitWaves];
+  __shared__ int s_hash[2 * kMaxSplitWaves];
   __shared__ int s_find[2];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nt = blockDim.x, B = a.B;
   const int n_waves = nt >> 6;
@@ -1427,7 +1429,7 @@ void decode_fused_kernel(DecodeArgs a, AppendArgs ap, int mode) {
   KernargPtr pa = (KernargPtr)__builtin_amdgcn_kernarg_segment_ptr();
   asm volatile("" : "+s"(pa));
   const DecodeArgs a2 = *pa;
-  stream_range<R, VF, true, LO>(a2, w_id, s_ids, s_rec, s_len, n_steps);
+  stream_range<R, VF, true, LO, NWV>(a2, w_id, s_ids, s_rec, s_len, n_steps);
 #endif
 }
 
@@ -1778,9 +1780,18 @@ static int launch_split(const DecodeArgs &a, hipStream_t s) {
 template <int R>
 static void launch_fused_ring(const DecodeArgs &a, const AppendArgs &ap, int mode, dim3 grid,
                               dim3 block, hipStream_t s) {
-  if (a.kv_fp8)
-    hipLaunchKernelGGL((decode_fused_kernel<R, 2>), grid, block, 0, s, a, ap, mode);
-  else if (a.vs)
+  if (a.kv_fp8) {
+    // The e4m3 stream is bound by its waves' instructions (half the bytes per
+    // step, the same math plus the code conversions): two waves per SIMD, one
+    // kv head each, cover each other's dependency chains; at 256 registers
+    // the ring is 2 steps deep (3 would spill). Measured 125.1 against
+    // 130.9 us at config 2; the bf16 and int8-V streams, bound by their
+    // loads, measured level or slower this way.
+    hipLaunchKernelGGL((decode_fused_kernel<2, 2, false, kMaxSplitWaves>), grid,
+                       dim3(64 * std::min(kMaxSplitWaves, a.n_kv_heads)), 0, s, a, ap, mode);
+    return;
+  }
+  if (a.vs)
     hipLaunchKernelGGL((decode_fused_kernel<R, 1>), grid, block, 0, s, a, ap, mode);
   else
     hipLaunchKernelGGL((decode_fused_kernel<R, 0>), grid, block, 0, s, a, ap, mode);
