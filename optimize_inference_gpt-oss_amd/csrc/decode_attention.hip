@@ -90,6 +90,7 @@ constexpr int kSplitWaves = 4;         // split kernel: one wave per SIMD
 constexpr int kStageRecs = 8;          // finished segments a stream wave holds in LDS
 constexpr int kSplitThreads = 64 * kSplitWaves;
 constexpr int kMaxSplitWaves = 8;      // the fused kernel's 8-wave form: two waves per SIMD
+constexpr int kShortRangeTokens = 256; // stream per workgroup up to which that form is used
 constexpr int kPrepThreads = 1024;
 constexpr int kMaxBatch = 8192;        // sequences per call (prefix sums kept in LDS)
 constexpr int kBadBlock = -1;          // F entry: id outside the pool
@@ -158,7 +159,7 @@ __device__ __forceinline__ int seq_tokens(const DecodeArgs &a, int b, bool *over
   return max(min(n, cap), 0);
 }
 
-__device__ __forceinline__ int pad_step(int n) { return (n + kStep - 1) & ~(kStep - 1); }
+__host__ __device__ __forceinline__ int pad_step(int n) { return (n + kStep - 1) & ~(kStep - 1); }
 
 // The ranges of the stream (T tokens, whole steps of 32). S > 0: range k is
 // [k S, (k + 1) S) (a forced split size); S = 0: the n ranges split the T / 32
@@ -1789,6 +1790,22 @@ static void launch_fused_ring(const DecodeArgs &a, const AppendArgs &ap, int mod
     // loads, measured level or slower this way.
     hipLaunchKernelGGL((decode_fused_kernel<2, 2, false, kMaxSplitWaves>), grid,
                        dim3(64 * std::min(kMaxSplitWaves, a.n_kv_heads)), 0, s, a, ap, mode);
+    return;
+  }
+  // Short ranges (at most kShortRangeTokens of stream per workgroup, bounded
+  // on the host from the shape: a window layer of a large batch) are bound by
+  // the prologue and each step's chain, not by their loads: the 8-wave form
+  // too (config 3: bf16 37.4 -> 35.5 us, int8 V 32.5 -> 30.0 us; with 512
+  // tokens per range, config 5's window layers, it is slower).
+  const int64_t range_bound = ((int64_t)a.B * pad_step(a.max_len) + a.n_wg - 1) / a.n_wg;
+  if (a.n_kv_heads == kMaxSplitWaves && a.fixed_S == 0 && range_bound <= kShortRangeTokens) {
+    const dim3 b8(64 * kMaxSplitWaves);
+    if (a.vs)
+      hipLaunchKernelGGL((decode_fused_kernel<2, 1, false, kMaxSplitWaves>), grid, b8, 0, s, a,
+                         ap, mode);
+    else
+      hipLaunchKernelGGL((decode_fused_kernel<2, 0, false, kMaxSplitWaves>), grid, b8, 0, s, a,
+                         ap, mode);
     return;
   }
   if (a.vs)
