@@ -86,3 +86,15 @@ def test_fp8_large_scores_and_tiny_heads(gkv, cuda, torch_mod):
     case = DecodeCase(16, 64, 8, L, window=0, scale=2.5, seed=85, sink_scale=6.0,
                       kv_fp8=True)
     check(case, run(case, gkv, torch_mod, cuda, False))
+
+
+@pytest.mark.parametrize("hq,hkv,window", [(16, 2, 0), (12, 3, 128), (8, 4, 0), (8, 4, 128)])
+def test_fp8_fewer_kv_heads(gkv, cuda, torch_mod, hq, hkv, window):
+    """Fewer than 8 kv heads (the e4m3 launch's workgroup then has one wave per
+    kv head) and group sizes 8, 4 and 2, on full and window layers."""
+    rng = np.random.default_rng(86 + hkv)
+    B = 40
+    L = rng.integers(0, 1500, size=B).astype(np.int32)
+    L[:3] = [0, 1, 127]
+    case = DecodeCase(B, hq, hkv, L, window=window, scale=0.5, seed=87 + hkv, kv_fp8=True)
+    check(case, run(case, gkv, torch_mod, cuda, True))
